@@ -1,0 +1,160 @@
+"""Random-init Mixtral-shaped weights for the benchmark configs.
+
+No checkpoint is available offline, so every config runs on synthetic
+weights: matrices N(0, std) in bf16 (std 0.02), RMSNorm weights ones (the
+init of ``_RMSNorm`` at ``megakernels/mixtral/model.py:120-124``), residual
+inputs N(0, 1).  The object returned by :func:`make_synthetic_mixtral` is
+duck-typed like the reference's ``MixtralForCausalLM`` as far as
+``make_globals`` needs (``.config``, ``.device``, ``.dtype``,
+``.stacked_params``, ``.lm_head``, ``.stacked_kv_cache``, ``.model``), with
+the stacked layout of ``megakernels/mixtral/model.py:486-565``: ``expert_gate``
+= HF ``w1`` ``[L, E, F, H]``, ``expert_up`` = ``w3`` ``[L, E, F, H]``,
+``expert_down`` = ``w2`` ``[L, E, H, F]``, ``router_weight`` ``[L, E, H]``.
+
+Attention, LM-head and KV-cache tensors are empty placeholders: the MoE hot
+path never reads them.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, replace
+from types import SimpleNamespace
+from typing import Optional
+
+import torch
+
+
+@dataclass(frozen=True)
+class MoEConfig:
+    num_hidden_layers: int
+    hidden_size: int
+    intermediate_size: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    num_local_experts: int
+    num_experts_per_tok: int
+    vocab_size: int
+    rms_norm_eps: float = 1e-5
+
+
+#: BASELINE config 1: small MoE decode layer (plumbing; MALL-resident)
+C1 = MoEConfig(1, 1024, 3584, 8, 2, 8, 2, 32000)
+#: BASELINE config 2: one full-size Mixtral-8x7B MoE layer
+C2 = MoEConfig(1, 4096, 14336, 32, 8, 8, 2, 32000)
+#: the reference's small debug shapes (demos/mixtral/debug_mixtral_mk.py:38-48)
+SMALL = MoEConfig(1, 512, 1024, 8, 2, 4, 2, 256)
+
+CONFIGS = {"c1": C1, "c2": C2, "small": SMALL}
+
+
+@dataclass
+class StackedMoEParams:
+    qkv_proj: torch.Tensor
+    attn_ln_weight: torch.Tensor
+    o_proj: torch.Tensor
+    ffn_ln_weight: torch.Tensor
+    router_weight: torch.Tensor
+    expert_gate: torch.Tensor
+    expert_up: torch.Tensor
+    expert_down: torch.Tensor
+    router_bias: Optional[torch.Tensor] = None
+    predictor_weight: Optional[torch.Tensor] = None
+
+
+def _normal(shape, std, gen, device, dtype=torch.bfloat16):
+    return torch.empty(shape, dtype=dtype, device=device).normal_(0.0, std, generator=gen)
+
+
+def make_synthetic_mixtral(
+    config: MoEConfig,
+    device="cpu",
+    seed: int = 0,
+    std: float = 0.02,
+    ln_weight_std: float | None = None,
+    router_bias: Optional[list[float]] = None,
+    predictor_sigma: float | None = None,
+):
+    """Build stacked random weights for ``config`` on ``device``.
+
+    ``ln_weight_std`` draws the FFN RMSNorm weights as ``1 + N(0, s)`` instead
+    of ones (exercises the norm-weight rounding step in tests).
+    ``router_bias`` (per-expert list) and ``predictor_sigma`` (noise std on a
+    predictor copy of the router) enable the two optional extensions.
+    """
+    device = torch.device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    L, H, F, E = (config.num_hidden_layers, config.hidden_size,
+                  config.intermediate_size, config.num_local_experts)
+    dt = torch.bfloat16
+    router = _normal([L, E, H], std, gen, device)
+    gate = _normal([L, E, F, H], std, gen, device)
+    up = _normal([L, E, F, H], std, gen, device)
+    down = _normal([L, E, H, F], std, gen, device)
+    if ln_weight_std is None:
+        ffn_ln = torch.ones([L, H], dtype=dt, device=device)
+    else:
+        ffn_ln = (1.0 + _normal([L, H], ln_weight_std, gen, device, torch.float32)).to(dt)
+    bias = None
+    if router_bias is not None:
+        bias = torch.tensor(router_bias, dtype=torch.float32, device=device).expand(L, E).contiguous()
+    predictor = None
+    if predictor_sigma is not None:
+        predictor = (router.float() + _normal([L, E, H], predictor_sigma, gen, device, torch.float32)).to(dt)
+    empty = torch.empty(0, dtype=dt, device=device)
+    params = StackedMoEParams(
+        qkv_proj=empty, attn_ln_weight=empty, o_proj=empty, ffn_ln_weight=ffn_ln,
+        router_weight=router, expert_gate=gate, expert_up=up, expert_down=down,
+        router_bias=bias, predictor_weight=predictor,
+    )
+    return SimpleNamespace(
+        config=config,
+        device=device,
+        dtype=dt,
+        stacked_params=params,
+        lm_head=SimpleNamespace(input_norm=SimpleNamespace(weight=torch.ones(H, dtype=dt, device=device)),
+                                lm_head=SimpleNamespace(weight=empty)),
+        stacked_kv_cache=(empty, empty),
+        model=SimpleNamespace(rope_cos=torch.empty(0, device=device), rope_sin=torch.empty(0, device=device)),
+        # the seeded stream continues here: residual inputs are drawn after
+        # the weights, so they are independent of every weight row
+        generator=gen,
+    )
+
+
+def make_residuals(n_tokens: int, hidden: int, generator: torch.Generator | None = None, seed: int = 0,
+                   device=None) -> torch.Tensor:
+    """``n_tokens`` residual inputs N(0, 1) in bf16, ``[n, H]``, drawn from
+    ``generator`` (normally ``model.generator``, continuing the weight stream)
+    or, without one, from a fresh generator seeded ``seed``."""
+    if generator is None:
+        generator = torch.Generator(device=torch.device(device or "cpu"))
+        generator.manual_seed(seed)
+    dev = generator.device
+    return torch.empty([n_tokens, hidden], dtype=torch.bfloat16, device=dev).normal_(0.0, 1.0, generator=generator)
+
+
+def with_layers(config: MoEConfig, layers: int) -> MoEConfig:
+    return replace(config, num_hidden_layers=layers)
+
+
+def to_device(model, device):
+    """Copy of a synthetic model with every tensor moved to ``device``."""
+    device = torch.device(device)
+
+    def mv(t):
+        return None if t is None else t.to(device)
+
+    sp = model.stacked_params
+    params = StackedMoEParams(**{k: mv(v) for k, v in vars(sp).items()})
+    return SimpleNamespace(
+        config=model.config,
+        device=device,
+        dtype=model.dtype,
+        stacked_params=params,
+        lm_head=SimpleNamespace(input_norm=SimpleNamespace(weight=mv(model.lm_head.input_norm.weight)),
+                                lm_head=SimpleNamespace(weight=mv(model.lm_head.lm_head.weight))),
+        stacked_kv_cache=tuple(mv(t) for t in model.stacked_kv_cache),
+        model=SimpleNamespace(rope_cos=mv(model.model.rope_cos), rope_sin=mv(model.model.rope_sin)),
+        generator=None,
+    )

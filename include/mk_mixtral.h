@@ -1,0 +1,201 @@
+/*
+ * mk_mixtral.h -- C ABI of the MI355X (gfx950) persistent MoE decode
+ * megakernel.
+ *
+ * Replaces the reference's pybind11 binding `mk_mixtral(...)`
+ * (demos/mixtral/mixtral.cu:28-94), whose argument order is the field order
+ * of `mixtral_globals` (demos/mixtral/mixtral.cuh:153-203) and of the Python
+ * caller `interpret_with_mk` (megakernels/mixtral/mk.py:42-96).  The struct
+ * below keeps that field order; tensors become raw device pointers plus the
+ * dimensions the reference bakes in at compile time
+ * (demos/mixtral/mixtral.cuh:22-35).
+ *
+ * Conventions
+ *   - bf16 tensors are passed as `uint16_t *` (raw bf16 bit patterns).
+ *   - Every pointer is a device pointer on the current HIP device, except
+ *     where noted.  The caller owns all memory; the kernel only borrows it.
+ *   - Launches are asynchronous on `stream` (a `hipStream_t`, NULL = default
+ *     stream).  Entry points never throw; they return an `mk_status_code`.
+ *   - The caller zeroes (or pre-fills) `barriers` before each launch, as the
+ *     reference's callers do (megakernels/generators.py:115-116,132).
+ *
+ * Instruction queues: `instructions[num_workers][queue_len][32]` int32, the
+ * serialised layout of megakernels/instructions.py:97-119.  Worker w (one
+ * workgroup, one compute unit) runs queue w in order.  Implemented opcodes:
+ *   0 NoOp
+ *   5 RmsRouterUpgate           [5, layer, start_block, num_blocks]
+ *   6 ExpertDownProjFused       [6, layer, start_block, end_block, reduction_block=0]
+ *   8 SpeculativeExpertPredict  [8, layer]
+ * Opcodes 1-4 and 7 (attention, LM head) are rejected with
+ * MK_ERR_UNSUPPORTED_OPCODE.
+ *
+ * Barriers: `barriers[bar_layers][bar_ops][bar_width]` int32, counter for
+ * (layer, opcode) at [layer][opcode-1][0].  Waits proceed once a counter is
+ * >= the expected arrival count (so pre-filled barriers satisfy them):
+ *   opcode 5 waits [l][3][0] >= hidden / o_proj_block_size
+ *   opcode 6 waits [l][4][0] >= intermediate / expert_proj_block_size
+ *   opcode 8 waits [l-1][5][0] >= k * hidden / down_proj_block_size (l > 0)
+ * and arrive with +num_blocks, +k*(end-start), +1 respectively
+ * (megakernels/mixtral/python_vm.py:38-54,228-371).
+ *
+ * Device-side failures (barrier spin time-out, bad opcode or operand) are
+ * recorded in a status word and make every worker exit; they are read back
+ * with mk_mixtral_read_status().
+ */
+#ifndef MK_MIXTRAL_H
+#define MK_MIXTRAL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MK_MIXTRAL_ABI_VERSION 1
+#define MK_INTS_PER_INSTRUCTION 32
+#define MK_TIMING_SLOTS 128
+#define MK_STATUS_WORDS 16
+#define MK_MAX_EXPERTS 16
+
+typedef enum mk_status_code {
+    MK_OK = 0,
+    MK_ERR_INVALID_ARGUMENT = 1,  /* host validation failed                   */
+    MK_ERR_UNSUPPORTED = 2,       /* shape outside what the kernel implements */
+    MK_ERR_HIP = 3,               /* HIP runtime error, see mk_mixtral_last_hip_error */
+    MK_ERR_NOT_CORESIDENT = 4,    /* grid cannot be fully resident            */
+    MK_ERR_TIMEOUT = 16,          /* device: barrier spin timed out           */
+    MK_ERR_BAD_OPCODE = 17,       /* device: opcode not in 0..8               */
+    MK_ERR_UNSUPPORTED_OPCODE = 18, /* device: opcode 1-4 or 7                */
+    MK_ERR_BAD_INSTRUCTION = 19   /* device: operand out of range             */
+} mk_status_code;
+
+/* Status words written by the kernel (first failure wins):
+ * [0] code, [1] worker, [2] queue slot, [3] opcode, [4] layer,
+ * [5] expected count / bad word index, [6] observed count / bad value. */
+enum {
+    MK_STATUS_CODE = 0,
+    MK_STATUS_WORKER = 1,
+    MK_STATUS_SLOT = 2,
+    MK_STATUS_OPCODE = 3,
+    MK_STATUS_LAYER = 4,
+    MK_STATUS_EXPECTED = 5,
+    MK_STATUS_SEEN = 6
+};
+
+/* Timing slots (subset of include/util.cuh:220-252 of the reference), in
+ * 100 MHz s_memrealtime ticks (low 32 bits, global clock shared by all
+ * compute units) when timing is enabled. */
+enum {
+    MK_TEVENT_START = 0,
+    MK_TEVENT_END = 4,
+    MK_TEVENT_AT_GMEM_WAIT = 44,
+    MK_TEVENT_DONE_GMEM_WAIT = 45,
+    MK_TEVENT_AT_GMEM_STORE = 46,
+    MK_TEVENT_DONE_GMEM_STORE = 47,
+    MK_TEVENT_FIRST_LOAD = 48,
+    MK_TEVENT_FIRST_USE = 49
+};
+
+typedef struct mk_mixtral_globals {
+    uint32_t struct_size;          /* sizeof(mk_mixtral_globals) */
+    uint32_t abi_version;          /* MK_MIXTRAL_ABI_VERSION */
+
+    /* megakernel internals (mixtral.cuh:155-157) */
+    int32_t *barriers;             /* [bar_layers, bar_ops, bar_width] */
+    int64_t bar_layers, bar_ops, bar_width;
+    const int32_t *instructions;   /* [num_workers, queue_len, 32] */
+    int64_t num_workers, queue_len;
+    int32_t *timings;              /* [num_workers, queue_len, 128] or NULL */
+
+    /* attention weights (mixtral.cuh:160-162): accepted, unused by 0/5/6/8 */
+    const void *qkv_weights;
+    const void *attn_norm_weights;
+    const void *o_weights;
+
+    /* MoE weights (mixtral.cuh:165-169), bf16, row-major */
+    const uint16_t *expert_gate_weights;  /* [L*E, F, H] */
+    const uint16_t *expert_up_weights;    /* [L*E, F, H] */
+    const uint16_t *expert_down_weights;  /* [L*E, H, F] */
+    const uint16_t *router_weights;       /* [L*E, H]    */
+    const uint16_t *ffn_ln_weights;       /* [L, H]      */
+
+    /* LM head, KV cache, RoPE (mixtral.cuh:172-181): accepted, unused */
+    const void *lm_head_norm_weights;
+    const void *lm_head_weights;
+    const void *k_cache;
+    const void *v_cache;
+    const float *rope_cos;
+    const float *rope_sin;
+
+    /* activations (mixtral.cuh:184-191) */
+    uint16_t *hidden_states;       /* [H] bf16, updated in place by opcode 6 */
+    void *q_post_rope;
+    void *attn_out;
+    float *attn_lse_intermediates;
+    float *attn_out_intermediates;
+    uint16_t *expert_silu_out;     /* [E, F] bf16 */
+    uint16_t *router_normed_hidden;/* [H] bf16 */
+    void *logits;
+
+    /* router outputs (mixtral.cuh:194-198) */
+    int32_t *selected_expert_indices;   /* [k] */
+    uint16_t *selected_expert_scores;   /* [k] bf16 */
+    int32_t *predicted_expert_indices;  /* [k] */
+
+    /* scalars (mixtral.cuh:201-204) */
+    uint32_t pos_id;
+    float attn_scale;
+    float rms_norm_eps;
+    int32_t skip_attn_reduction;
+
+    /* dimensions compiled into the reference kernel (mixtral.cuh:22-35) */
+    int32_t num_layers;
+    int32_t hidden_size;           /* H, multiple of 512 */
+    int32_t intermediate_size;     /* F, multiple of 512 */
+    int32_t num_experts;           /* E, 2..16 */
+    int32_t num_experts_per_tok;   /* k, must be 2 */
+
+    /* block sizes (MixtralGlobals fields, megakernels/mixtral/scheduler.py:144-151) */
+    int32_t expert_proj_block_size;
+    int32_t down_proj_block_size;
+    int32_t o_proj_block_size;
+
+    /* extensions, no counterpart in the reference; NULL keeps its semantics */
+    const float *router_bias;          /* [L*E] fp32 added to router logits  */
+    const uint16_t *predictor_weights; /* [L*E, H] bf16 for opcode 8        */
+
+    /* control */
+    int32_t *status;               /* device int32[16], NULL = library-owned buffer */
+    uint32_t spin_timeout_us;      /* barrier spin limit, 0 = 2 s            */
+    int32_t record_timings;        /* nonzero: write timing slots           */
+} mk_mixtral_globals;
+
+/* Launch one persistent-kernel pass over the instruction queues.
+ * Replaces the pybind11 `mk_mixtral` (demos/mixtral/mixtral.cu:28-94). */
+int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream);
+
+/* Copy the library-owned status words of `device` into out[16] after a
+ * device-wide synchronisation.  No reference counterpart (the reference has
+ * no device-side error reporting). */
+int mk_mixtral_read_status(int device, int32_t *out);
+
+/* Zero the library-owned status words of `device` (synchronous). */
+int mk_mixtral_clear_status(int device);
+
+/* Number of compute units and the largest worker count that can be
+ * co-resident for this kernel.  Counterpart of get_sm_count
+ * (megakernels/utils.py:133-135). */
+int mk_mixtral_query_device(int device, int32_t *num_cus, int32_t *max_workers);
+
+const char *mk_mixtral_error_string(int code);
+/* hipError_t and the name of the HIP call behind the last MK_ERR_HIP on the
+ * calling thread. */
+int mk_mixtral_last_hip_error(void);
+const char *mk_mixtral_last_error_site(void);
+int mk_mixtral_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MK_MIXTRAL_H */

@@ -1,0 +1,165 @@
+"""Shared test harness: one MoE decode layer run on the GPU through the
+reference-shaped launcher and on the CPU through the oracle PyVM, from the
+same weights, inputs and instruction list.
+
+Tolerances: expert indices bit-exact; hidden states and
+SiLU outputs within max-abs-rel 2e-2, where
+``max_abs_rel(y, r) = max|y - r| / max(max|r|, 1e-6)`` per token; the barrier
+tensor equal to the oracle's.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from megakernels_amd.mixtral.scheduler import make_globals, make_moe_dag, prefill_oproj_barrier
+from megakernels_amd.mixtral.synthetic import make_residuals, make_synthetic_mixtral, to_device
+from megakernels_amd.scheduler import Schedule, assign_to_sms, tensorize_instructions
+from oracle import python_vm as oracle
+
+TOL = 2e-2
+MARGIN = 1e-3
+
+
+def max_abs_rel(y: torch.Tensor, r: torch.Tensor) -> float:
+    y = y.detach().float().cpu()
+    r = r.detach().float().cpu()
+    if r.numel() == 0:
+        return 0.0
+    return float((y - r).abs().max() / max(float(r.abs().max()), 1e-6))
+
+
+def mean_rdiff(a: torch.Tensor, b: torch.Tensor) -> float:
+    """The reference's diff metric (megakernels/instructions.py:72-80)."""
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    return float((2 * (a - b).abs() / (a.abs() + b.abs() + 1e-6)).mean())
+
+
+def router_margins(model, residual: torch.Tensor, layer: int = 0):
+    """(|l1 - l2|, |l2 - l3|) of the oracle's sorted router logits."""
+    sp = model.stacked_params
+    normed = oracle.rms_norm(residual, sp.ffn_ln_weight[layer], model.config.rms_norm_eps)
+    bias = None if sp.router_bias is None else sp.router_bias[layer]
+    logits = oracle.router_logits(sp.router_weight[layer], normed, bias)
+    top = torch.sort(logits, descending=True).values
+    return float(top[0] - top[1]), float(top[1] - top[2])
+
+
+def draw_tokens(model, n: int, margin: float = MARGIN, max_draws: int | None = None) -> torch.Tensor:
+    """Draw residuals one at a time from the model's seeded stream, redrawing
+    any whose top-3 router logits are within ``margin`` (so the selected
+    expert pair, including its order, is unambiguous)."""
+    H = model.config.hidden_size
+    out = []
+    draws = 0
+    limit = max_draws or 20 * n
+    while len(out) < n:
+        if draws >= limit:
+            raise RuntimeError("too many rejected draws")
+        x = make_residuals(1, H, generator=model.generator)[0]
+        draws += 1
+        m01, m12 = router_margins(model, x)
+        if m01 >= margin and m12 >= margin:
+            out.append(x)
+    return torch.stack(out)
+
+
+@dataclass
+class TokenResult:
+    indices_gpu: list
+    indices_ref: list
+    err_hidden: float
+    err_silu: float
+    err_normed: float
+    scores_gpu: list
+    scores_ref: list
+    barriers_equal: bool
+    predicted_gpu: list
+    predicted_ref: list
+
+    def assert_ok(self, tol: float = TOL):
+        assert self.indices_gpu == self.indices_ref, f"indices {self.indices_gpu} != oracle {self.indices_ref}"
+        assert self.err_hidden <= tol, f"hidden max-abs-rel {self.err_hidden:.3e} > {tol}"
+        assert self.err_silu <= tol, f"silu max-abs-rel {self.err_silu:.3e} > {tol}"
+        assert self.err_normed <= tol, f"normed max-abs-rel {self.err_normed:.3e} > {tol}"
+        for a, b in zip(self.scores_gpu, self.scores_ref):
+            assert abs(a - b) <= 2 ** -7 * max(abs(b), 1e-3), f"scores {self.scores_gpu} vs {self.scores_ref}"
+        assert self.barriers_equal, "barrier tensor differs from the oracle's"
+
+
+class MoECase:
+    """Weights on CPU (oracle) and GPU (kernel), one schedule for both."""
+
+    def __init__(self, config, seed=0, device="cuda", workers=None, ln_weight_std=None, router_bias=None,
+                 predictor_sigma=None, expert_proj_block_size=None, down_proj_block_size=None,
+                 predict=False, mode="rr", generate_on_device=False, stop_after_op=None):
+        dev = torch.device(device)
+        gen_dev = dev if generate_on_device else torch.device("cpu")
+        model = make_synthetic_mixtral(config, gen_dev, seed, ln_weight_std=ln_weight_std,
+                                       router_bias=router_bias, predictor_sigma=predictor_sigma)
+        if generate_on_device:
+            self.gpu_model = model
+            self.cpu_model = to_device(model, "cpu")
+            self.cpu_model.generator = torch.Generator().manual_seed(seed + 1)
+        else:
+            self.cpu_model = model
+            self.gpu_model = to_device(model, dev)
+        self.device = dev
+        self.config = config
+        if workers is None:
+            workers = torch.cuda.get_device_properties(dev).multi_processor_count
+        kw = dict(sm_count=workers, expert_proj_block_size=expert_proj_block_size,
+                  down_proj_block_size=down_proj_block_size)
+        self.g_gpu = make_globals(self.gpu_model, **kw)
+        self.g_cpu = make_globals(self.cpu_model, **kw)
+        nodes, end = make_moe_dag(self.g_gpu, predict=predict, stop_after_op=stop_after_op)
+        self.schedule = Schedule(self.g_gpu, nodes, end)
+        tensorize_instructions(self.g_gpu, assign_to_sms(mode, schedule=self.schedule))
+        self.linear = self.schedule.get_linear_instructions()
+        self.stop_after_op = stop_after_op
+
+    def reset(self, residual: torch.Tensor):
+        for g, dev in ((self.g_cpu, "cpu"), (self.g_gpu, self.device)):
+            g.barriers.zero_()
+            prefill_oproj_barrier(g)
+            g.expert_silu_out.zero_()
+            g.router_normed_hidden.zero_()
+            g.hidden_states.copy_(residual.to(dev))
+
+    def run_gpu(self, **kw):
+        import mk_mixtral
+        from megakernels_amd.mixtral.mk import interpret_with_mk
+
+        kw.setdefault("debug_sync", True)
+        interpret_with_mk(self.g_gpu, mk_mixtral.mk_mixtral, **kw)
+        torch.cuda.synchronize(self.device)
+
+    def run_oracle(self):
+        oracle.interpret_with_pyvm(self.g_cpu, self.linear)
+
+    def compare(self) -> TokenResult:
+        g, r = self.g_gpu, self.g_cpu
+        idx_ref = r.selected_expert_indices.long()
+        silu_gpu = g.expert_silu_out.cpu()[idx_ref]
+        silu_ref = r.expert_silu_out[idx_ref]
+        return TokenResult(
+            indices_gpu=g.selected_expert_indices.cpu().tolist(),
+            indices_ref=r.selected_expert_indices.tolist(),
+            err_hidden=max_abs_rel(g.hidden_states, r.hidden_states),
+            err_silu=max_abs_rel(silu_gpu, silu_ref),
+            err_normed=max_abs_rel(g.router_normed_hidden, r.router_normed_hidden),
+            scores_gpu=g.selected_expert_scores.float().cpu().tolist(),
+            scores_ref=r.selected_expert_scores.float().tolist(),
+            barriers_equal=torch.equal(g.barriers.cpu(), r.barriers),
+            predicted_gpu=g.predicted_expert_indices.cpu().tolist(),
+            predicted_ref=r.predicted_expert_indices.tolist(),
+        )
+
+    def run_token(self, residual: torch.Tensor, **kw) -> TokenResult:
+        self.reset(residual)
+        self.run_gpu(**kw)
+        self.run_oracle()
+        return self.compare()
