@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""Benchmark: batch-1 Mixtral-8x7B MoE decode layer on one MI355X.
+
+Workload (uniform): one full-size Mixtral MoE layer
+(hidden 4096, FFN 14336, 8 experts, top-2), bf16 weights N(0, 0.02), 1024
+independent batch-1 decode tokens with residual inputs N(0, 1), all resident
+in HBM before timing.  One *step* = the 1024 tokens, each a separate launch of
+the persistent kernel (opcodes 5 and 6 over all 256 compute units), updating
+its residual in place.  ``value`` is decode tokens/s through the layer.
+
+Also reported: MoE-layer microseconds per launch (HIP events on the launch
+stream, averaged over the timed region, plus a per-launch median/p10/p90
+pass), the HBM roofline fraction of the layer (algorithmic bytes
+2*(E*H + H + k*3*F*H) / time / 8 TB/s), the skewed-routing variant (+2.0
+router bias on experts 0 and 1), and the CPU oracle timed on the host.
+
+``python bench.py --gpus 1 --steps 10 --warmup 2``
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "epic-kernel_amd", ROOT):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "batch-1 decode tokens/s, Mixtral-8x7B shape; MoE layer µs; % HBM peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def moe_layer_bytes(cfg) -> int:
+    """Algorithmic HBM bytes of one MoE layer: router + ffn RMSNorm weights +
+    k experts x {gate, up, down}, bf16."""
+    E, H, F, k = cfg.num_local_experts, cfg.hidden_size, cfg.intermediate_size, cfg.num_experts_per_tok
+    return 2 * (E * H + H + k * 3 * F * H)
+
+
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+class MoEBench:
+    """Per-token launches of the MoE-only schedule over resident inputs."""
+
+    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None):
+        import torch
+
+        import mk_mixtral
+        from megakernels_amd.mixtral.scheduler import make_globals, make_moe_dag, expected_oproj_arrivals
+        from megakernels_amd.mixtral.synthetic import make_residuals, make_synthetic_mixtral
+        from megakernels_amd.scheduler import Schedule, assign_to_sms, tensorize_instructions
+
+        self.torch = torch
+        self.dev = torch.device("cuda:0")
+        self.cfg = cfg
+        self.tokens = tokens
+        self.model = make_synthetic_mixtral(cfg, self.dev, seed, router_bias=router_bias)
+        self.residuals = make_residuals(tokens, cfg.hidden_size, generator=self.model.generator)
+        self.globs = g = make_globals(self.model)
+        nodes, end = make_moe_dag(g)
+        self.schedule = Schedule(g, nodes, end)
+        tensorize_instructions(g, assign_to_sms("rr", schedule=self.schedule))
+        # one barrier tensor and one residual row per token, so a step needs
+        # no per-token resets between launches
+        bars = torch.zeros([tokens, *g.barriers.shape], dtype=torch.int32, device=self.dev)
+        bars[:, 0, 3, 0] = expected_oproj_arrivals(g)
+        self.bars_init = bars
+        self.bars = bars.clone()
+        self.work = self.residuals.clone()
+
+        from megakernels_amd.mixtral.mk import interpret_with_mk
+
+        captured = {}
+
+        def capture(*args, **kw):
+            kw.pop("stream", None)
+            captured["g"] = mk_mixtral.build_globals_struct(*args, **kw)
+
+        interpret_with_mk(g, capture)
+        self.struct = captured["g"]
+        self.lib = mk_mixtral.load_library()
+        self.mk = mk_mixtral
+        self.row_bytes = self.work.stride(0) * 2
+        self.bar_bytes = self.bars.stride(0) * 4
+
+    def _launch(self, t: int, stream_ptr):
+        s = self.struct
+        s.hidden_states = self.work.data_ptr() + t * self.row_bytes
+        s.barriers = self.bars.data_ptr() + t * self.bar_bytes
+        rc = self.lib.mk_mixtral_launch(ctypes.byref(s), stream_ptr)
+        if rc:
+            raise self.mk.MKError(rc, self.lib.mk_mixtral_error_string(rc).decode())
+
+    def step(self):
+        self.work.copy_(self.residuals)
+        self.bars.copy_(self.bars_init)
+        stream = ctypes.c_void_p(self.torch.cuda.current_stream(self.dev).cuda_stream)
+        for t in range(self.tokens):
+            self._launch(t, stream)
+
+    def per_launch_us(self, n: int):
+        """Event-timed individual launches (median/p10/p90 in microseconds)."""
+        torch = self.torch
+        self.work.copy_(self.residuals)
+        self.bars.copy_(self.bars_init)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for t in range(n):
+            evs[t][0].record()
+            self._launch(t % self.tokens, stream)
+            evs[t][1].record()
+        torch.cuda.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+        return {"median": statistics.median(us), "p10": us[int(0.1 * (n - 1))], "p90": us[int(0.9 * (n - 1))],
+                "min": us[0]}
+
+    def check_status(self):
+        self.mk.raise_if_failed(self.dev)
+
+
+def run_timed(bench, steps: int, warmup: int):
+    torch = bench.torch
+    for _ in range(warmup):
+        bench.step()
+    torch.cuda.synchronize()
+    bench.check_status()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        bench.step()
+    stop.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    bench.check_status()
+    wall = t1 - t0
+    launches = steps * bench.tokens
+    gpu_s = start.elapsed_time(stop) / 1e3
+    return {"wall_s": wall, "gpu_s": gpu_s, "launches": launches, "us_per_launch_events": gpu_s / launches * 1e6}
+
+
+def cpu_baseline(bench, seconds: float, threads: int):
+    """The CPU oracle (restated python_vm, C + OpenMP) on the same weights,
+    inputs and instruction list, over a bounded sample of tokens."""
+    import torch
+
+    from megakernels_amd.mixtral.scheduler import make_globals, prefill_oproj_barrier
+    from megakernels_amd.mixtral.synthetic import to_device
+    from oracle import python_vm as oracle
+
+    oracle.set_num_threads(threads)
+    cpu_model = to_device(bench.model, "cpu")
+    g = make_globals(cpu_model, sm_count=bench.globs.sm_count())
+    linear = bench.schedule.get_linear_instructions()
+    residuals = bench.residuals.cpu()
+    done = 0
+    agree = 0
+    t0 = time.perf_counter()
+    while done < bench.tokens and (done == 0 or time.perf_counter() - t0 < seconds):
+        g.barriers.zero_()
+        prefill_oproj_barrier(g)
+        g.hidden_states.copy_(residuals[done])
+        oracle.interpret_with_pyvm(g, linear)
+        done += 1
+    elapsed = time.perf_counter() - t0
+    # selection parity of the sampled tokens against the kernel
+    for t in range(done):
+        bench.work[t].copy_(bench.residuals[t])
+        bench.bars[t].copy_(bench.bars_init[t])
+    stream = ctypes.c_void_p(torch.cuda.current_stream(bench.dev).cuda_stream)
+    sel = []
+    for t in range(done):
+        bench._launch(t, stream)
+        sel.append(bench.globs.selected_expert_indices.clone())
+    torch.cuda.synchronize()
+    for t in range(done):
+        g.barriers.zero_()
+        prefill_oproj_barrier(g)
+        g.hidden_states.copy_(residuals[t])
+        oracle.interpret_with_pyvm(g, linear)
+        agree += int(torch.equal(sel[t].cpu(), g.selected_expert_indices))
+    return {
+        "value": done / elapsed,
+        "unit": "tokens/s",
+        "cores": oracle.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} config-2 tokens through the oracle python_vm restatement (opcodes 5+6, "
+                  f"{len(linear)} instructions each, C+OpenMP), {elapsed:.1f} s",
+        "moe_layer_us": elapsed / done * 1e6,
+        "cpu_model": cpu_model_name(),
+        "os_cpu_count": os.cpu_count(),
+        "selection_agrees_with_gpu": f"{agree}/{done}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--tokens", type=int, default=1024)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--no-skewed", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU design is described in DESIGN.md and is not benchmarked", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from megakernels_amd.mixtral.synthetic import C1, C2
+
+    cfg = C2 if args.config == "c2" else C1
+    print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
+    bench = MoEBench(cfg, args.tokens, seed=0)
+    timed = run_timed(bench, args.steps, args.warmup)
+    dist = bench.per_launch_us(256)
+    nbytes = moe_layer_bytes(cfg)
+    us = timed["us_per_launch_events"]
+    achieved = nbytes / (us * 1e-6) / 1e9
+    print(f"bench: uniform {us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+
+    skewed = None
+    if not args.no_skewed:
+        sk = MoEBench(cfg, args.tokens, seed=0,
+                      router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
+        sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
+        sk_us = sk_timed["us_per_launch_events"]
+        skewed = {"moe_layer_us": sk_us, "hbm_frac": nbytes / (sk_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                  "router_bias": "+2.0 on experts 0 and 1"}
+        del sk
+        torch.cuda.empty_cache()
+        print(f"bench: skewed {sk_us:.2f} us/launch", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or os.cpu_count()
+        print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(bench, args.cpu_seconds, threads)
+
+    g = bench.globs
+    out = {
+        "metric": METRIC,
+        "value": bench.tokens * args.steps / timed["wall_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": timed["wall_s"] / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"BASELINE config {'2' if args.config == 'c2' else '1'} uniform: one Mixtral-8x7B-shaped "
+                        f"MoE layer (hidden {cfg.hidden_size}, FFN {cfg.intermediate_size}, "
+                        f"{cfg.num_local_experts} experts, top-{cfg.num_experts_per_tok}), {bench.tokens} "
+                        "batch-1 decode tokens per step, one persistent-kernel launch per token",
+            "tokens_per_step": bench.tokens,
+            "workers": g.sm_count(),
+            "expert_proj_block_size": g.expert_proj_block_size,
+            "down_proj_block_size": g.down_proj_block_size,
+        },
+        "moe_layer_us": us,
+        "moe_layer_us_per_launch": dist,
+        "hbm_frac": achieved / HBM_PEAK_GBS,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "bytes_per_launch": nbytes,
+            "kernel": "mk_mixtral_kernel",
+        },
+        "skewed": skewed,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
