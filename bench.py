@@ -58,7 +58,7 @@ def cpu_model_name() -> str:
 class MoEBench:
     """Per-token launches of the MoE-only schedule over resident inputs."""
 
-    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None):
+    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, static_partition: bool = False):
         import torch
 
         import mk_mixtral
@@ -92,7 +92,7 @@ class MoEBench:
             kw.pop("stream", None)
             captured["g"] = mk_mixtral.build_globals_struct(*args, **kw)
 
-        interpret_with_mk(g, capture)
+        interpret_with_mk(g, capture, static_partition=static_partition)
         self.struct = captured["g"]
         self.lib = mk_mixtral.load_library()
         self.mk = mk_mixtral
@@ -221,6 +221,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--static-partition", action="store_true",
+                    help="each instruction processes only its own rows (no work sharing)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -234,7 +236,7 @@ def main():
 
     cfg = C2 if args.config == "c2" else C1
     print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
-    bench = MoEBench(cfg, args.tokens, seed=0)
+    bench = MoEBench(cfg, args.tokens, seed=0, static_partition=args.static_partition)
     timed = run_timed(bench, args.steps, args.warmup)
     dist = bench.per_launch_us(256)
     nbytes = moe_layer_bytes(cfg)
@@ -244,7 +246,7 @@ def main():
 
     skewed = None
     if not args.no_skewed:
-        sk = MoEBench(cfg, args.tokens, seed=0,
+        sk = MoEBench(cfg, args.tokens, seed=0, static_partition=args.static_partition,
                       router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
         sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
         sk_us = sk_timed["us_per_launch_events"]
@@ -283,6 +285,7 @@ def main():
             "workers": g.sm_count(),
             "expert_proj_block_size": g.expert_proj_block_size,
             "down_proj_block_size": g.down_proj_block_size,
+            "work_sharing": not args.static_partition,
         },
         "moe_layer_us": us,
         "moe_layer_us_per_launch": dist,

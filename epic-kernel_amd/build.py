@@ -4,7 +4,9 @@
 
 Flags: ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the
 compiler from emitting packed-fp32 VALU instructions; the host pass warns that
-it does not know the feature, which is harmless.  ``MK_THREADS`` (workgroup
+it does not know the feature, which is harmless.  The AMDGPU atomic optimizer
+is off: all atomics are single-lane, and its wave-aggregated rewrite would
+force a wait for each work-claim atomic right where it is issued.  ``MK_THREADS`` (workgroup
 size) and ``MK_NT_LOADS`` (non-temporal weight loads) are tuning knobs.
 """
 
@@ -39,6 +41,10 @@ def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -
         "-fPIC",
         "-shared",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # every atomic in the kernel is issued by one lane; the wave-aggregating
+        # rewrite would broadcast each result right after the atomic and so
+        # stall the work-claiming look-ahead on the atomic's round trip
+        "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
         f"-I{REPO / 'include'}",
     ]
     for k, v in (defines or {}).items():

@@ -2,9 +2,15 @@
 //
 // One workgroup per compute unit runs its instruction queue in order
 // (instruction layout: megakernels/instructions.py:97-119).  Workers meet only
-// through int32 counters in HBM: an arrival is an agent-scope release
-// fetch-add, a wait is a bounded spin of relaxed agent-scope loads followed by
-// one agent-scope acquire fence.  There is no loader/consumer/storer split as
+// through int32 counters in HBM.  Data that one workgroup produces and
+// another consumes within a launch (SiLU rows, hidden rows, router outputs)
+// is written with agent-scope (device-coherent, write-through) stores and
+// read with agent-scope loads; an arrival is all waves' stores completed
+// (s_waitcnt) followed by a relaxed agent-scope fetch-add, and a wait is a
+// bounded spin of relaxed agent-scope loads.  No L2 write-back or invalidate
+// is issued: on MI355X those serialise per XCD and cost ~15 us each when all
+// compute units issue them together, while the coherent accesses cost well
+// under a microsecond.  There is no loader/consumer/storer split as
 // in the reference's warp-specialised VM (include/megakernel.cuh:118-140):
 // every wave issues its own 16-byte weight loads and does its own math.
 //
@@ -39,13 +45,27 @@
 #include "mk_mixtral.h"
 
 #ifndef MK_THREADS
-#define MK_THREADS 1024
+#define MK_THREADS 512
 #endif
 #ifndef MK_NT_LOADS
 #define MK_NT_LOADS 1
 #endif
 #ifndef MK_DOT2_BUILTIN
 #define MK_DOT2_BUILTIN 0
+#endif
+// Items at the end of each opcode-5 instruction that are claimed through its
+// cursor (and so can be taken by other workers); the rest run statically.
+#ifndef MK_TAIL_ITEMS
+#define MK_TAIL_ITEMS 32
+#endif
+// Spin back-off: a waiting workgroup polls its counter every ~64 * N clocks,
+// N growing from 1 to MK_SPIN_SLEEP_MAX, so hundreds of idle workgroups do not
+// keep the counter's memory channel busy while others still stream weights.
+#ifndef MK_SPIN_SLEEP_MAX
+#define MK_SPIN_SLEEP_MAX 16
+#endif
+#ifndef MK_CLAIM_LOOKAHEAD
+#define MK_CLAIM_LOOKAHEAD 1
 #endif
 
 namespace {
@@ -57,6 +77,13 @@ constexpr int kChunkElems = 512;  // bf16 columns covered by one wave-wide 16 B/
 // workgroup per compute unit, so a grid of #CU workers covers every CU once.
 constexpr int kMinLdsBytes = 84 * 1024;
 constexpr uint32_t kTicksPerUs = 100;  // s_memrealtime runs at 100 MHz
+constexpr int kCachePolicySc1 = 16;     // buffer-load cache policy: device scope
+// Work-sharing scratch (int32): [0] exit counter, then a (cursor, done) pair
+// per instruction slot w * queue_len + q.
+constexpr int kScratchJobBase = 16;
+constexpr int kMaxHelpCandidates = 1024;
+constexpr int kRowBatchLds = 64;  // rows per opcode-6 batch (partial sums in LDS)
+constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 16 * 512)
 
 static_assert(kThreads % 64 == 0 && kThreads <= 1024, "wave64 workgroup");
 
@@ -87,16 +114,24 @@ struct KParams {
     int32_t expert_bs, down_bs, oproj_bs;
     float eps;
     uint32_t timeout_ticks;
+    int32_t *scratch;
+    int32_t work_sharing;
 };
 
 // Per-workgroup state that outlives a single instruction.
 struct SharedState {
     float red[kWaves * MK_MAX_EXPERTS];
-    float logits[MK_MAX_EXPERTS];
+    float red_ss[kWaves];
+    float bias[MK_MAX_EXPERTS];
     int route_layer;  // layer whose routing below was computed here, -1 none
     int route_idx[2];
     float route_score[2];  // bf16 score values widened to fp32
     int flag;
+    int dbg_own, dbg_help, dbg_rounds;  // work-sharing counters for the timing record
+    int next_item;                      // per-instruction item counter shared by the waves
+    float part[kRowBatchLds * 2 * kMaxSegments];  // opcode-6 partial sums: [row][slot][segment]
+    int ncand;
+    int cand[kMaxHelpCandidates];
 };
 
 struct Ctx {
@@ -118,6 +153,35 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// Device-coherent accesses for data shared between workgroups of a launch.
+__device__ __forceinline__ void st_dev16(uint16_t *p, uint32_t v) {
+    __hip_atomic_store(p, (uint16_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev32(void *p, uint32_t v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev16(const uint16_t *p) {
+    return __hip_atomic_load(const_cast<uint16_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev32(const void *p) {
+    return __hip_atomic_load(const_cast<uint32_t *>(reinterpret_cast<const uint32_t *>(p)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16-byte device-coherent load of base + byte_off (base uniform across the
+// wave): a raw buffer load with the sc1 cache policy.
+__device__ __forceinline__ u32x4 ld_dev128(const void *base, uint32_t byte_off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCachePolicySc1);
+}
+__device__ __forceinline__ void st_dev128(u32x4 *p, u32x4 v) {
+    uint32_t *q = reinterpret_cast<uint32_t *>(p);
+    st_dev32(q, v.x);
+    st_dev32(q + 1, v.y);
+    st_dev32(q + 2, v.z);
+    st_dev32(q + 3, v.w);
+}
 
 __device__ __forceinline__ u32x4 load_stream(const u32x4 *p) {
 #if MK_NT_LOADS
@@ -150,14 +214,27 @@ __device__ __forceinline__ float dot8(u32x4 w, u32x4 a, float acc) {
     return acc;
 }
 
-// Butterfly sum over the 64 lanes; every lane ends with the same value
-// (each step adds the same two operands on both partner lanes).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_add_src(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
 }
 
+// Sum over the 64 lanes with DPP: pairs within quads, quads, half rows,
+// rows (16 lanes), then row 0 -> 1 and 2 -> 3 (row_bcast15) and rows 0-1 ->
+// 2-3 (row_bcast31); lane 63 holds the total, which is returned to every
+// lane.  Fixed order, so the result is deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_add_src<0xb1>(v);        // quad_perm [1, 0, 3, 2]
+    v += dpp_add_src<0x4e>(v);        // quad_perm [2, 3, 0, 1]
+    v += dpp_add_src<0x141>(v);       // row_half_mirror
+    v += dpp_add_src<0x140>(v);       // row_mirror
+    v += dpp_add_src<0x142, 0xa>(v);  // row_bcast15 into rows 1 and 3
+    v += dpp_add_src<0x143, 0xc>(v);  // row_bcast31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Workgroup sum.  `red` must not be reused before the next workgroup
+// barrier.
 __device__ __forceinline__ float block_sum(float v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     v = wave_sum(v);
@@ -166,7 +243,6 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) s += red[i];
-    __syncthreads();
     return s;
 }
 
@@ -209,7 +285,6 @@ __device__ void report_error(const KParams &p, int code, const Ctx &c, int opcod
         p.status[MK_STATUS_LAYER] = layer;
         p.status[MK_STATUS_EXPECTED] = expected;
         p.status[MK_STATUS_SEEN] = seen;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     }
 }
 
@@ -222,8 +297,10 @@ __device__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int exp
         int v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (v < expected) {
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            int nap = 1;
             for (;;) {
-                __builtin_amdgcn_s_sleep(1);
+                for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
+                if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
                 v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (v >= expected) break;
                 if (aborted(p)) {
@@ -237,7 +314,6 @@ __device__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int exp
                 }
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         sh.flag = ok;
     }
     __syncthreads();
@@ -246,16 +322,15 @@ __device__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int exp
     return ok;
 }
 
-// Make every wave's global stores complete, then join the workgroup.  A
-// workgroup barrier alone does not wait for outstanding stores of other
-// waves, and the release below only writes back what has reached L2.
+// Make every wave's global stores complete, then join the workgroup (a
+// workgroup barrier alone does not wait for other waves' outstanding stores).
 __device__ __forceinline__ void drain_and_sync() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 }
 
 __device__ __forceinline__ void arrive(int32_t *ctr, int n) {
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, n, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -304,54 +379,123 @@ __device__ __forceinline__ void dot_pair(const uint16_t *row_a, const uint16_t *
 // RMSNorm + router (shared by opcodes 5 and 8)
 // ---------------------------------------------------------------------------
 
-// normed hidden (bf16) -> act[0 .. H/8); router logits -> sh.logits[0 .. E).
-__device__ void rms_router(const KParams &p, SharedState &sh, u32x4 *act, int layer, const uint16_t *router) {
-    const int tid = threadIdx.x;
-    const int nv = p.H >> 3;
-    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(p.hidden);
-    const u32x4 *w4 = reinterpret_cast<const u32x4 *>(p.ffn_ln + (size_t)layer * p.H);
+// Expert-count specialisation: kE > 0 compiles for exactly kE experts (the
+// Mixtral case, branch-free loops); kE == 0 handles any 2 <= E <= 16 at
+// run time.
+template <int kE>
+struct Experts {
+    static constexpr int kMax = kE > 0 ? kE : MK_MAX_EXPERTS;
+    __device__ static __forceinline__ bool has(const KParams &p, int e) { return kE > 0 ? e < kE : e < p.E; }
+};
 
-    float ss = 0.f;
-    for (int v = tid; v < nv; v += kThreads) {
-        const u32x4 x = x4[v];
-        ss += sumsq2(x.x) + sumsq2(x.y) + sumsq2(x.z) + sumsq2(x.w);
-    }
-    ss = block_sum(ss, sh.red);
-    const float r = 1.0f / sqrtf(ss / (float)p.H + p.eps);
+// Per-thread norm weights and router rows, loaded before the producer wait
+// (they do not depend on it), for the common case H / 8 <= threads: thread t
+// owns the 8 hidden elements [8t, 8t + 8).  Threads < E also stage the router
+// bias in LDS.
+template <int kE>
+struct RouterRegs {
+    u32x4 ln;
+    u32x4 rw[Experts<kE>::kMax];
+};
 
+__device__ __forceinline__ bool router_fits(const KParams &p) { return (p.H >> 3) <= kThreads; }
+
+template <int kE>
+__device__ __forceinline__ void router_prefetch(const KParams &p, SharedState &sh, int layer, const uint16_t *router,
+                                                RouterRegs<kE> &rr) {
+    const int v = threadIdx.x;
+    if (v < p.E) sh.bias[v] = p.router_bias != nullptr ? p.router_bias[layer * p.E + v] : 0.f;
+    if (!router_fits(p) || v >= (p.H >> 3)) return;
+    rr.ln = reinterpret_cast<const u32x4 *>(p.ffn_ln + (size_t)layer * p.H)[v];
     const uint16_t *rw = router + (size_t)layer * p.E * p.H;
-    float acc[MK_MAX_EXPERTS];
 #pragma unroll
-    for (int e = 0; e < MK_MAX_EXPERTS; ++e) acc[e] = 0.f;
-    for (int v = tid; v < nv; v += kThreads) {
-        const u32x4 x = x4[v], w = w4[v];
-        u32x4 n;
-        n.x = norm2(x.x, w.x, r);
-        n.y = norm2(x.y, w.y, r);
-        n.z = norm2(x.z, w.z, r);
-        n.w = norm2(x.w, w.w, r);
-        act[v] = n;
+    for (int e = 0; e < Experts<kE>::kMax; ++e)
+        if (Experts<kE>::has(p, e)) rr.rw[e] = reinterpret_cast<const u32x4 *>(rw + (size_t)e * p.H)[v];
+}
+
+__device__ __forceinline__ u32x4 norm8(u32x4 x, u32x4 w, float r) {
+    u32x4 n;
+    n.x = norm2(x.x, w.x, r);
+    n.y = norm2(x.y, w.y, r);
+    n.z = norm2(x.z, w.z, r);
+    n.w = norm2(x.w, w.w, r);
+    return n;
+}
+
+__device__ __forceinline__ float sumsq8(u32x4 x) { return sumsq2(x.x) + sumsq2(x.y) + sumsq2(x.z) + sumsq2(x.w); }
+
+// Reduce per-thread router partials to the E logits (+ bias).  Every thread
+// sums the per-wave partials itself, so the logits end up in registers after
+// a single workgroup barrier.
+template <int kE>
+__device__ void finish_logits(const KParams &p, SharedState &sh, const float *acc, float *logits) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-        for (int e = 0; e < MK_MAX_EXPERTS; ++e)
-            if (e < p.E) acc[e] = dot8(reinterpret_cast<const u32x4 *>(rw + (size_t)e * p.H)[v], n, acc[e]);
-    }
-    const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int e = 0; e < MK_MAX_EXPERTS; ++e) {
-        if (e < p.E) {
+    for (int e = 0; e < Experts<kE>::kMax; ++e) {
+        if (Experts<kE>::has(p, e)) {
             const float s = wave_sum(acc[e]);
             if (lane == 0) sh.red[e * kWaves + wave] = s;
         }
     }
     __syncthreads();
-    if (tid < p.E) {
-        float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < kWaves; ++i) s += sh.red[tid * kWaves + i];
-        if (p.router_bias != nullptr) s += p.router_bias[layer * p.E + tid];
-        sh.logits[tid] = s;
+    for (int e = 0; e < Experts<kE>::kMax; ++e) {
+        float s = 0.f;
+        if (Experts<kE>::has(p, e)) {
+#pragma unroll
+            for (int i = 0; i < kWaves; ++i) s += sh.red[e * kWaves + i];
+            s += sh.bias[e];
+        }
+        logits[e] = s;
     }
-    __syncthreads();
+}
+
+// normed hidden (bf16) -> act[0 .. H/8); router logits -> logits[0 .. E) in
+// every thread.  Reads hidden_states, so it runs after the producer wait.
+template <int kE>
+__device__ void rms_router(const KParams &p, SharedState &sh, u32x4 *act, int layer, const uint16_t *router,
+                           const RouterRegs<kE> &rr, int32_t *tim, float *logits) {
+    const int tid = threadIdx.x;
+    const int nv = p.H >> 3;
+    float acc[Experts<kE>::kMax];
+#pragma unroll
+    for (int e = 0; e < Experts<kE>::kMax; ++e) acc[e] = 0.f;
+
+    if (router_fits(p)) {
+        const bool mine = tid < nv;
+        u32x4 x = {0u, 0u, 0u, 0u};
+        if (mine) x = ld_dev128(p.hidden, (uint32_t)tid * 16u);
+        const float sq = sumsq8(x);
+        stamp(tim, 60);
+        const float ss = block_sum(sq, sh.red_ss);
+        stamp(tim, 61);
+        const float r = 1.0f / sqrtf(ss / (float)p.H + p.eps);
+        if (mine) {
+            const u32x4 n = norm8(x, rr.ln, r);
+            act[tid] = n;
+#pragma unroll
+            for (int e = 0; e < Experts<kE>::kMax; ++e)
+                if (Experts<kE>::has(p, e)) acc[e] = dot8(rr.rw[e], n, 0.f);
+        }
+    } else {
+        const u32x4 *w4 = reinterpret_cast<const u32x4 *>(p.ffn_ln + (size_t)layer * p.H);
+        float ss = 0.f;
+        for (int v = tid; v < nv; v += kThreads) ss += sumsq8(ld_dev128(p.hidden, (uint32_t)v * 16u));
+        ss = block_sum(ss, sh.red_ss);
+        const float r = 1.0f / sqrtf(ss / (float)p.H + p.eps);
+        const uint16_t *rw = router + (size_t)layer * p.E * p.H;
+        for (int v = tid; v < nv; v += kThreads) {
+            const u32x4 n = norm8(ld_dev128(p.hidden, (uint32_t)v * 16u), w4[v], r);
+            act[v] = n;
+#pragma unroll
+            for (int e = 0; e < Experts<kE>::kMax; ++e)
+                if (Experts<kE>::has(p, e))
+                    acc[e] = dot8(reinterpret_cast<const u32x4 *>(rw + (size_t)e * p.H)[v], n, acc[e]);
+        }
+    }
+    stamp(tim, 62);
+    finish_logits<kE>(p, sh, acc, logits);
+    stamp(tim, 63);
 }
 
 struct Top2 {
@@ -359,33 +503,158 @@ struct Top2 {
     float p0, p1;
 };
 
-// softmax over E logits, then the two largest probabilities in descending
-// order (strict comparison: the lower expert index wins a tie).
-__device__ Top2 softmax_top2(const float *logits, int E) {
-    float m = logits[0];
-    for (int e = 1; e < E; ++e) m = fmaxf(m, logits[e]);
-    float s = 0.f;
-    for (int e = 0; e < E; ++e) s += expf(logits[e] - m);
-    Top2 t{0, -1, expf(logits[0] - m) / s, -1.f};
-    for (int e = 1; e < E; ++e) {
-        const float pe = expf(logits[e] - m) / s;
-        if (pe > t.p0) {
-            t.i1 = t.i0;
-            t.p1 = t.p0;
-            t.i0 = e;
-            t.p0 = pe;
-        } else if (t.i1 < 0 || pe > t.p1) {
-            t.i1 = e;
-            t.p1 = pe;
+// Top-2 of softmax(logits) in descending order, and the two probabilities.
+// softmax is monotonic, so the pair is chosen on the logits (strict
+// comparison: the lower expert index wins a tie); p_i = exp(l_i - max) / sum
+// as torch.softmax computes it.
+template <int kE>
+__device__ Top2 softmax_top2(const KParams &p, const float *logits) {
+    int i0 = 0;
+    float l0 = logits[0];
+#pragma unroll
+    for (int e = 1; e < Experts<kE>::kMax; ++e) {
+        if (Experts<kE>::has(p, e) && logits[e] > l0) {
+            i0 = e;
+            l0 = logits[e];
         }
     }
-    return t;
+    int i1 = -1;
+    float l1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < Experts<kE>::kMax; ++e) {
+        if (Experts<kE>::has(p, e) && e != i0 && (i1 < 0 || logits[e] > l1)) {
+            i1 = e;
+            l1 = logits[e];
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < Experts<kE>::kMax; ++e)
+        if (Experts<kE>::has(p, e)) s += expf(logits[e] - l0);
+    return Top2{i0, i1, 1.0f / s, expf(l1 - l0) / s};
 }
 
 // ---------------------------------------------------------------------------
 // opcode 5: RmsRouterUpgate  (python_vm.py:228-277)
 // ---------------------------------------------------------------------------
 
+// Next item from the workgroup's LDS counter (uniform result).
+__device__ __forceinline__ int next_local_item(SharedState &sh, int lane) {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&sh.next_item, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+// One item of opcode 5: row r of the FFN dimension for expert slot j, i.e.
+// the gate and up rows (H bf16 each) dotted with the normed hidden state,
+// then silu_out[e][r] = bf16(bf16(silu(bf16(g))) * bf16(u)).
+__device__ __forceinline__ void upgate_item(const KParams &p, const u32x4 *act, int layer, int row0, int nrows,
+                                            int e0, int e1, int it, int lane) {
+    const int j = it >= nrows;
+    const int r = row0 + (j ? it - nrows : it);
+    const int e = j ? e1 : e0;
+    const size_t off = ((size_t)(layer * p.E + e) * p.F + r) * (size_t)p.H;
+    float ag = 0.f, au = 0.f;
+    dot_pair(p.gate + off, p.up + off, act, act, p.H / kChunkElems, lane, ag, au);
+    ag = wave_sum(ag);
+    au = wave_sum(au);
+    if (lane == 0) {
+        const float g = rbf(ag), u = rbf(au);
+        const float sg = rbf(g / (1.0f + expf(-g)));
+        st_dev16(p.silu + (size_t)e * p.F + r, f2bf(sg * u));
+    }
+}
+
+// Wave-level claim of the next item of an instruction.  Lane 0 issues the
+// atomic; the value is broadcast only where it is needed, so the wait for the
+// atomic's return can sit behind the current item's weight loads.
+__device__ __forceinline__ int claim_issue(int32_t *cursor, int lane) {
+    int v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(cursor, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+}
+
+// Items [first, first + count) of an opcode-5 instruction whose FFN rows
+// start at row0 (nrows rows, items 0 .. 2*nrows), claimed one at a time from
+// the instruction's cursor (the next claim is issued before the current
+// item's loads) until the cursor passes count.  Returns the number done here.
+__device__ int upgate_claimed(const KParams &p, const u32x4 *act, int layer, int row0, int nrows, int e0, int e1,
+                              int first, int count, int32_t *cursor, int lane) {
+    int done_here = 0;
+    int c = __builtin_amdgcn_readfirstlane(claim_issue(cursor, lane));
+    while (c < count) {
+#if MK_CLAIM_LOOKAHEAD
+        int next_raw = claim_issue(cursor, lane);
+        upgate_item(p, act, layer, row0, nrows, e0, e1, first + c, lane);
+        ++done_here;
+        // first use of the claim result: keeps the compiler from hoisting the
+        // broadcast (and the wait for the atomic) above the item's loads
+        asm volatile("" : "+v"(next_raw));
+        c = __builtin_amdgcn_readfirstlane(next_raw);
+#else
+        upgate_item(p, act, layer, row0, nrows, e0, e1, first + c, lane);
+        ++done_here;
+        c = __builtin_amdgcn_readfirstlane(claim_issue(cursor, lane));
+#endif
+    }
+    return done_here;
+}
+
+// Publish `n` finished items of an instruction after this wave's (coherent)
+// stores have completed.
+__device__ __forceinline__ void publish_done(int32_t *done, int n, int lane) {
+    if (n <= 0) return;
+    __builtin_amdgcn_s_waitcnt(0);
+    if (lane == 0) __hip_atomic_fetch_add(done, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int tail_items(int items) { return items < MK_TAIL_ITEMS ? items : MK_TAIL_ITEMS; }
+
+// After its own instruction, a workgroup helps the other opcode-5
+// instructions of the same layer (any worker, any queue slot) whose claimable
+// tails still have items.  It works in rounds: one parallel pass over the
+// instruction table reads every candidate's cursor (one round trip), then all
+// waves claim from one candidate picked by workgroup index, so helpers spread
+// over the unfinished instructions.  Routing is a deterministic function of
+// the layer's inputs, so the helper's experts are the owner's.
+__device__ void help_upgate(const KParams &p, SharedState &sh, const u32x4 *act, int layer, int self_slot, int e0,
+                            int e1) {
+    if (threadIdx.x == 0) sh.dbg_rounds = 0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int total = (int)gridDim.x * p.queue_len;
+    for (int round = 0; round < kMaxHelpCandidates; ++round) {
+        if (tid == 0) sh.ncand = 0;
+        __syncthreads();
+        for (int sl = tid; sl < total; sl += kThreads) {
+            const int32_t *ins = p.instructions + (size_t)sl * MK_INTS_PER_INSTRUCTION;
+            if (sl == self_slot || ins[0] != 5 || ins[1] != layer) continue;
+            const int start = ins[2], nb = ins[3];
+            if (start < 0 || nb <= 0 || (int64_t)(start + nb) * p.expert_bs > (int64_t)p.F) continue;
+            const int tail = tail_items(2 * nb * p.expert_bs);
+            if ((int)ld_dev32(p.scratch + kScratchJobBase + 2 * sl) >= tail) continue;
+            const int k = atomicAdd(&sh.ncand, 1);
+            if (k < kMaxHelpCandidates) sh.cand[k] = sl;
+        }
+        __syncthreads();
+        const int n = min(sh.ncand, kMaxHelpCandidates);
+        if (n == 0) break;
+        const int sl = __builtin_amdgcn_readfirstlane(sh.cand[((int)blockIdx.x + round) % n]);
+        const int32_t *ins = p.instructions + (size_t)sl * MK_INTS_PER_INSTRUCTION;
+        const int start = __builtin_amdgcn_readfirstlane(ins[2]);
+        const int nb = __builtin_amdgcn_readfirstlane(ins[3]);
+        const int items = 2 * nb * p.expert_bs;
+        const int tail = tail_items(items);
+        int32_t *cursor = p.scratch + kScratchJobBase + 2 * sl;
+        const int n_done = upgate_claimed(p, act, layer, start * p.expert_bs, nb * p.expert_bs, e0, e1,
+                                          items - tail, tail, cursor, lane);
+        publish_done(cursor + 1, n_done, lane);
+        if (lane == 0 && n_done) atomicAdd(&sh.dbg_help, n_done);
+        if (tid == 0) sh.dbg_rounds = round + 1;
+        __syncthreads();
+    }
+}
+
+template <int kE>
 __device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
                                      const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
@@ -396,12 +665,18 @@ __device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *a
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 5, layer, start, nb);
         return false;
     }
+    RouterRegs<kE> rr;
+    router_prefetch<kE>(p, sh, layer, p.router, rr);
+    // items 0 .. kWaves-1 go to waves 0 .. kWaves-1, the rest through the
+    // LDS counter (reset here; the wait below is a workgroup barrier)
+    if (threadIdx.x == 0) sh.next_item = kWaves;
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
-    rms_router(p, sh, act, layer, p.router);
-    const Top2 t = softmax_top2(sh.logits, p.E);
+    float logits[Experts<kE>::kMax];
+    rms_router<kE>(p, sh, act, layer, p.router, rr, tim, logits);
+    const Top2 t = softmax_top2<kE>(p, logits);
     const float psum = t.p0 + t.p1;
     const uint32_t sc0 = f2bf(t.p0 / psum), sc1 = f2bf(t.p1 / psum);
     const int tid = threadIdx.x;
@@ -416,43 +691,130 @@ __device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *a
     // normed hidden state and the routing decision.
     if (start == 0) {
         u32x4 *out = reinterpret_cast<u32x4 *>(p.normed_out);
-        for (int v = tid; v < (p.H >> 3); v += kThreads) out[v] = act[v];
+        for (int v = tid; v < (p.H >> 3); v += kThreads) st_dev128(out + v, act[v]);
         if (tid == 0) {
-            p.sel_idx[0] = t.i0;
-            p.sel_idx[1] = t.i1;
-            p.sel_score[0] = (uint16_t)sc0;
-            p.sel_score[1] = (uint16_t)sc1;
+            st_dev32(p.sel_idx, (uint32_t)t.i0);
+            st_dev32(p.sel_idx + 1, (uint32_t)t.i1);
+            st_dev16(p.sel_score, sc0);
+            st_dev16(p.sel_score + 1, sc1);
         }
     }
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
     const int lane = tid & 63, wave = tid >> 6;
     const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
-    const int nc = p.H / kChunkElems;
-    for (int it = wave; it < 2 * nrows; it += kWaves) {
-        const int j = it >= nrows;
-        const int r = row0 + (j ? it - nrows : it);
-        const int e = j ? t.i1 : t.i0;
-        const size_t off = ((size_t)(layer * p.E + e) * p.F + r) * (size_t)p.H;
-        float ag = 0.f, au = 0.f;
-        dot_pair(p.gate + off, p.up + off, act, act, nc, lane, ag, au);
-        ag = wave_sum(ag);
-        au = wave_sum(au);
-        if (lane == 0) {
-            const float g = rbf(ag), u = rbf(au);
-            const float sg = rbf(g / (1.0f + expf(-g)));
-            p.silu[(size_t)e * p.F + r] = (uint16_t)f2bf(sg * u);
+    if (p.work_sharing) {
+        const int self_slot = c.worker * p.queue_len + c.slot;
+        int32_t *cursor = p.scratch + kScratchJobBase + 2 * self_slot;
+        const int items = 2 * nrows;
+        const int tail = tail_items(items);
+        if (tid == 0) {
+            sh.dbg_own = 0;
+            sh.dbg_help = 0;
         }
+        __syncthreads();
+        int n_done = 0;
+        for (int it = wave; it < items - tail; it = next_local_item(sh, lane)) {
+            upgate_item(p, act, layer, row0, nrows, t.i0, t.i1, it, lane);
+            ++n_done;
+        }
+        n_done += upgate_claimed(p, act, layer, row0, nrows, t.i0, t.i1, items - tail, tail, cursor, lane);
+        publish_done(cursor + 1, n_done, lane);
+        if (lane == 0) atomicAdd(&sh.dbg_own, n_done);
+        __syncthreads();
+        // items taken by helpers must be finished before this instruction arrives
+        if (!wait_ge(p, sh, cursor + 1, items, c, 5, layer)) return false;
+        arrive(bar_at(p, layer, 5), nb);
+        stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+        help_upgate(p, sh, act, layer, self_slot, t.i0, t.i1);
+        __syncthreads();
+        if (tim != nullptr && tid == 0) {
+            tim[56] = sh.dbg_own;
+            tim[57] = sh.dbg_help;
+            tim[58] = sh.dbg_rounds;
+        }
+        stamp(tim, 59);
+    } else {
+        // Waves take items from a workgroup counter in LDS rather than a
+        // fixed stride: the memory pipeline favours older waves, so with a
+        // fixed split the youngest wave ends up finishing its last items
+        // alone.
+        int k = 0;
+        for (int it = wave; it < 2 * nrows; ++k) {
+            upgate_item(p, act, layer, row0, nrows, t.i0, t.i1, it, lane);
+            // per-item completion times of waves 0 and 7 (timing record only)
+            if (tim != nullptr && lane == 0 && (wave == 0 || wave == kWaves - 1) && k < 16)
+                tim[64 + (wave ? 16 : 0) + k] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
+            it = next_local_item(sh, lane);
+        }
+        drain_and_sync();
+        arrive(bar_at(p, layer, 5), nb);
+        stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     }
-    drain_and_sync();
-    arrive(bar_at(p, layer, 5), nb);
-    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
 
 // ---------------------------------------------------------------------------
 // opcode 6: ExpertDownProjFused  (python_vm.py:284-314)
 // ---------------------------------------------------------------------------
+
+// Up to N chunks (512 bf16 each) of one row, n of them used (n uniform).
+template <int N>
+struct RowRegs {
+    u32x4 w[N];
+};
+
+template <int N>
+__device__ __forceinline__ void load_row(RowRegs<N> &r, const u32x4 *w, int n) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (i < n) r.w[i] = load_stream(w + i * 64);
+}
+
+template <int N>
+__device__ __forceinline__ float dot_row_regs(const RowRegs<N> &r, const u32x4 *x, int n, float acc) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (i < n) acc = dot8(r.w[i], x[i * 64], acc);
+    return acc;
+}
+
+constexpr int kSegChunks = 16;   // max chunks per opcode-6 item (16 KiB per wave)
+constexpr int kEarlyChunks = 8;  // chunks of its first item each wave loads before the opcode-6 wait
+constexpr int kRowBatch = kRowBatchLds;
+
+struct DownItem {
+    int row, slot, c0, n;  // batch-relative row, expert slot, first chunk, chunks
+};
+
+// Item `it` of a batch: row it / (2 S), expert slot (it / S) % 2, segment
+// it % S of a row split into S segments of nc / S (+1) chunks.
+__device__ __forceinline__ DownItem down_item(int it, int S, int nc) {
+    const int seg = it % S;
+    const int c0 = seg * nc / S, c1 = (seg + 1) * nc / S;
+    return DownItem{it / (2 * S), (it / S) & 1, c0, c1 - c0};
+}
+
+// Partial dot of one item; with use_pre, its first kEarlyChunks chunks are
+// already in `pre`.
+__device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 *xact, const DownItem &d, int lane,
+                                               bool use_pre, const RowRegs<kEarlyChunks> &pre) {
+    const u32x4 *w = reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane;
+    const u32x4 *x = xact + d.c0 * 64 + lane;
+    float acc = 0.f;
+    int done = 0;
+    if (use_pre) {
+        const int n = min(d.n, kEarlyChunks);
+        acc = dot_row_regs<kEarlyChunks>(pre, x, n, acc);
+        done = n;
+    }
+    if (done < d.n) {
+        RowRegs<kSegChunks> r;
+        load_row<kSegChunks>(r, w + done * 64, d.n - done);
+        acc = dot_row_regs<kSegChunks>(r, x + done * 64, d.n - done, acc);
+    }
+    return acc;
+}
 
 __device__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
                                    const Ctx &c, int32_t *tim) {
@@ -465,57 +827,88 @@ __device__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 6, layer, start, end);
         return false;
     }
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = start * p.down_bs, nrows = (end - start) * p.down_bs;
+    const int nc = p.F / kChunkElems;
+    const int S = (nc + kSegChunks - 1) / kSegChunks;  // column segments per row
+
+    // Early loads: when this workgroup routed the layer itself (opcode 5 ran
+    // here), the experts are known before the barrier, so each wave starts
+    // streaming the first chunks of its first item while it waits.
+    const bool known = sh.route_layer == layer;
+    const int first_batch = min(nrows, kRowBatch);
+    const bool early = known && wave < first_batch * 2 * S;
+    RowRegs<kEarlyChunks> pre;
+    if (early) {
+        const DownItem d = down_item(wave, S, nc);
+        const int e = sh.route_idx[d.slot];
+        const uint16_t *row = p.down + ((size_t)(layer * p.E + e) * p.H + row0 + d.row) * (size_t)p.F;
+        load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane, min(d.n, kEarlyChunks));
+    }
+
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
     int e0, e1;
     float s0, s1;
-    if (sh.route_layer == layer) {
+    if (known) {
         e0 = sh.route_idx[0];
         e1 = sh.route_idx[1];
         s0 = sh.route_score[0];
         s1 = sh.route_score[1];
     } else {
-        e0 = __builtin_amdgcn_readfirstlane(p.sel_idx[0]);
-        e1 = __builtin_amdgcn_readfirstlane(p.sel_idx[1]);
-        s0 = bf2f(p.sel_score[0]);
-        s1 = bf2f(p.sel_score[1]);
+        e0 = __builtin_amdgcn_readfirstlane((int)ld_dev32(p.sel_idx));
+        e1 = __builtin_amdgcn_readfirstlane((int)ld_dev32(p.sel_idx + 1));
+        s0 = bf2f(ld_dev16(p.sel_score));
+        s1 = bf2f(ld_dev16(p.sel_score + 1));
     }
     if (e0 < 0 || e0 >= p.E || e1 < 0 || e1 >= p.E) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 6, layer, e0, e1);
         return false;
     }
 
-    const int tid = threadIdx.x;
     const int nv = p.F >> 3;
-    const u32x4 *a0 = reinterpret_cast<const u32x4 *>(p.silu + (size_t)e0 * p.F);
-    const u32x4 *a1 = reinterpret_cast<const u32x4 *>(p.silu + (size_t)e1 * p.F);
+    const uint16_t *a0 = p.silu + (size_t)e0 * p.F;
+    const uint16_t *a1 = p.silu + (size_t)e1 * p.F;
     for (int v = tid; v < nv; v += kThreads) {
-        act[v] = a0[v];
-        act[nv + v] = a1[v];
+        act[v] = ld_dev128(a0, (uint32_t)v * 16u);
+        act[nv + v] = ld_dev128(a1, (uint32_t)v * 16u);
     }
+    if (tid == 0) sh.next_item = kWaves;
     __syncthreads();
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
-    const int lane = tid & 63, wave = tid >> 6;
-    const int row0 = start * p.down_bs, nrows = (end - start) * p.down_bs;
-    const int nc = p.F / kChunkElems;
     const size_t base0 = (size_t)(layer * p.E + e0) * p.H;
     const size_t base1 = (size_t)(layer * p.E + e1) * p.H;
-    for (int it = wave; it < nrows; it += kWaves) {
-        const int r = row0 + it;
-        float d0 = 0.f, d1 = 0.f;
-        dot_pair(p.down + (base0 + r) * (size_t)p.F, p.down + (base1 + r) * (size_t)p.F, act, act + nv, nc, lane,
-                 d0, d1);
-        d0 = wave_sum(d0);
-        d1 = wave_sum(d1);
-        if (lane == 0) {
-            float h = bf2f(p.hidden[r]);
+    for (int b0 = 0; b0 < nrows; b0 += kRowBatch) {
+        const int nb_rows = min(kRowBatch, nrows - b0);
+        const int items = nb_rows * 2 * S;
+        // items 0 .. kWaves-1 by wave index (their first chunks may be
+        // preloaded), the rest claimed from the LDS counter
+        for (int it = wave; it < items; it = next_local_item(sh, lane)) {
+            const DownItem d = down_item(it, S, nc);
+            const uint16_t *row = p.down + ((d.slot ? base1 : base0) + row0 + b0 + d.row) * (size_t)p.F;
+            const bool use_pre = early && b0 == 0 && it == wave;
+            const float acc = wave_sum(down_item_dot(row, act + (d.slot ? nv : 0), d, lane, use_pre, pre));
+            if (lane == 0) sh.part[(d.row * 2 + d.slot) * kMaxSegments + (it % S)] = acc;
+        }
+        __syncthreads();
+        // h = bf16(h + bf16(s_j * bf16(d_j))) for j = 0, 1 in order
+        for (int r = tid; r < nb_rows; r += kThreads) {
+            float d0 = 0.f, d1 = 0.f;
+            for (int sg = 0; sg < S; ++sg) {
+                d0 += sh.part[(r * 2 + 0) * kMaxSegments + sg];
+                d1 += sh.part[(r * 2 + 1) * kMaxSegments + sg];
+            }
+            uint16_t *hp = p.hidden + row0 + b0 + r;
+            float h = bf2f(ld_dev16(hp));
             h = rbf(h + rbf(s0 * rbf(d0)));
             h = rbf(h + rbf(s1 * rbf(d1)));
-            p.hidden[r] = (uint16_t)f2bf(h);
+            st_dev16(hp, f2bf(h));
         }
+        if (tid == 0) sh.next_item = kWaves;
+        __syncthreads();
     }
     drain_and_sync();
     arrive(bar_at(p, layer, 6), 2 * (end - start));
@@ -527,6 +920,7 @@ __device__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act
 // opcode 8: SpeculativeExpertPredict  (python_vm.py:356-371)
 // ---------------------------------------------------------------------------
 
+template <int kE>
 __device__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
@@ -534,16 +928,20 @@ __device__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const 
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 8, layer, 0, 0);
         return false;
     }
+    const uint16_t *weights = p.predictor != nullptr ? p.predictor : p.router;
+    RouterRegs<kE> rr;
+    router_prefetch<kE>(p, sh, layer, weights, rr);
     if (layer > 0) {
         stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
         if (!wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 8, layer)) return false;
         stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     }
-    rms_router(p, sh, act, layer, p.predictor != nullptr ? p.predictor : p.router);
-    const Top2 t = softmax_top2(sh.logits, p.E);
+    float logits[Experts<kE>::kMax];
+    rms_router<kE>(p, sh, act, layer, weights, rr, tim, logits);
+    const Top2 t = softmax_top2<kE>(p, logits);
     if (threadIdx.x == 0) {
-        p.pred_idx[0] = t.i0;
-        p.pred_idx[1] = t.i1;
+        st_dev32(p.pred_idx, (uint32_t)t.i0);
+        st_dev32(p.pred_idx + 1, (uint32_t)t.i1);
     }
     drain_and_sync();
     arrive(bar_at(p, layer, 8), 1);
@@ -555,6 +953,7 @@ __device__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const 
 // the persistent interpreter
 // ---------------------------------------------------------------------------
 
+template <int kE>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
@@ -572,9 +971,9 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         bool ok = true;
         switch (op) {
         case 0: break;
-        case 5: ok = op_rms_router_upgate(p, sh, act, ins, c, tim); break;
+        case 5: ok = op_rms_router_upgate<kE>(p, sh, act, ins, c, tim); break;
         case 6: ok = op_expert_downproj(p, sh, act, ins, c, tim); break;
-        case 8: ok = op_predict(p, sh, act, ins, c, tim); break;
+        case 8: ok = op_predict<kE>(p, sh, act, ins, c, tim); break;
         case 1:
         case 2:
         case 3:
@@ -591,6 +990,22 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         stamp(tim, MK_TEVENT_END);
         if (!ok) break;
     }
+
+    // Exit protocol: the last workgroup out (failed or not) zeroes the
+    // work-sharing counters for the next launch.  Every other workgroup has
+    // finished all of its scratch accesses before it increments the counter.
+    drain_and_sync();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(p.scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.flag = prev == (int)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (sh.flag) {
+        const int n = 2 * (int)gridDim.x * p.queue_len;
+        for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchJobBase + i] = 0;
+        drain_and_sync();
+        if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -604,6 +1019,8 @@ struct DeviceState {
     int num_cus = 0;
     int max_lds = 0;
     int32_t *status = nullptr;
+    int32_t *scratch = nullptr;
+    size_t scratch_ints = 0;
 };
 
 std::mutex g_mutex;
@@ -675,7 +1092,7 @@ int validate(const mk_mixtral_globals *g) {
     if (g->num_experts_per_tok != 2 || g->num_experts < 2 || g->num_experts > MK_MAX_EXPERTS)
         return MK_ERR_UNSUPPORTED;
     if (g->hidden_size < kChunkElems || g->hidden_size % kChunkElems || g->intermediate_size < kChunkElems ||
-        g->intermediate_size % kChunkElems)
+        g->intermediate_size % kChunkElems || g->intermediate_size > kMaxSegments * kSegChunks * kChunkElems)
         return MK_ERR_UNSUPPORTED;
     if (g->expert_proj_block_size < 1 || g->down_proj_block_size < 1 || g->o_proj_block_size < 1 ||
         g->intermediate_size % g->expert_proj_block_size || g->hidden_size % g->down_proj_block_size ||
@@ -725,7 +1142,7 @@ int mk_mixtral_query_device(int device, int32_t *num_cus, int32_t *max_workers) 
     if (rc != MK_OK) return rc;
     int blocks = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &blocks, reinterpret_cast<const void *>(mk_mixtral_kernel), kThreads, kMinLdsBytes);
+        &blocks, reinterpret_cast<const void *>(mk_mixtral_kernel<0>), kThreads, kMinLdsBytes);
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (num_cus) *num_cus = st->num_cus;
     if (max_workers) *max_workers = blocks * st->num_cus;
@@ -745,10 +1162,34 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const size_t lds = lds_bytes_for(g);
     if (lds + sizeof(SharedState) > (size_t)st->max_lds) return MK_ERR_UNSUPPORTED;
     int blocks = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void *>(mk_mixtral_kernel),
-                                                     kThreads, lds);
+    // Mixtral's 8 experts get a kernel specialised for exactly 8
+    const bool e8 = g->num_experts == 8;
+    const void *fn = e8 ? reinterpret_cast<const void *>(mk_mixtral_kernel<8>)
+                        : reinterpret_cast<const void *>(mk_mixtral_kernel<0>);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds);
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (g->num_workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
+
+    // work-sharing counters: exit counter + (cursor, done) per instruction slot
+    const size_t need = kScratchJobBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len;
+    if (need > st->scratch_ints) {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (need > st->scratch_ints) {
+            size_t cap = st->scratch_ints ? st->scratch_ints : 4096;
+            while (cap < need) cap *= 2;
+            if (st->scratch != nullptr) {
+                // kernels queued earlier may still use the old buffer
+                if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+                if ((e = hipFree(st->scratch)) != hipSuccess) return hip_fail(e, "hipFree");
+                st->scratch = nullptr;
+                st->scratch_ints = 0;
+            }
+            if ((e = hipMalloc(reinterpret_cast<void **>(&st->scratch), cap * sizeof(int32_t))) != hipSuccess)
+                return hip_fail(e, "hipMalloc");
+            if ((e = hipMemset(st->scratch, 0, cap * sizeof(int32_t))) != hipSuccess) return hip_fail(e, "hipMemset");
+            st->scratch_ints = cap;
+        }
+    }
 
     KParams kp;
     kp.instructions = g->instructions;
@@ -782,9 +1223,15 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const uint64_t us = g->spin_timeout_us ? g->spin_timeout_us : 2000000u;
     const uint64_t ticks = us * kTicksPerUs;
     kp.timeout_ticks = ticks > 0xffffffffu ? 0xffffffffu : (uint32_t)ticks;
+    kp.scratch = st->scratch;
+    kp.work_sharing = g->static_partition ? 0 : 1;
 
-    hipLaunchKernelGGL(mk_mixtral_kernel, dim3((unsigned)g->num_workers), dim3(kThreads), lds,
-                       reinterpret_cast<hipStream_t>(stream), kp);
+    if (e8)
+        hipLaunchKernelGGL(mk_mixtral_kernel<8>, dim3((unsigned)g->num_workers), dim3(kThreads), lds,
+                           reinterpret_cast<hipStream_t>(stream), kp);
+    else
+        hipLaunchKernelGGL(mk_mixtral_kernel<0>, dim3((unsigned)g->num_workers), dim3(kThreads), lds,
+                           reinterpret_cast<hipStream_t>(stream), kp);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "hipGetLastError");
     return MK_OK;

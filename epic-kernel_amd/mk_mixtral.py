@@ -20,6 +20,9 @@ sizes are the compile-time 16):
     bound on every in-kernel barrier wait (default 2 s);
 ``record_timings``
     write per-instruction ``s_memrealtime`` stamps into ``timings``;
+``static_partition``
+    process exactly each instruction's own rows (no work sharing between
+    workers; results and barrier counts are the same either way);
 ``debug_sync``
     synchronise after the launch and raise :class:`MKDeviceError` if the
     kernel recorded a failure.
@@ -142,6 +145,7 @@ class MkMixtralGlobals(ctypes.Structure):
         ("status", _P),
         ("spin_timeout_us", ctypes.c_uint32),
         ("record_timings", ctypes.c_int32),
+        ("static_partition", ctypes.c_int32),
     ]
 
 
@@ -287,6 +291,7 @@ def build_globals_struct(
     status=None,
     spin_timeout_us: int = 0,
     record_timings: bool = False,
+    static_partition: bool = False,
 ) -> MkMixtralGlobals:
     """Validate the reference-ordered arguments and fill the C struct.
 
@@ -383,6 +388,7 @@ def build_globals_struct(
     g.status = None if status is None else status.data_ptr()
     g.spin_timeout_us = int(spin_timeout_us)
     g.record_timings = int(bool(record_timings))
+    g.static_partition = int(bool(static_partition))
     return g
 
 
