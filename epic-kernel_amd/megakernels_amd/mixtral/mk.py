@@ -43,7 +43,8 @@ def interpret_with_mk(globs: MixtralGlobals, mk_func, **launch_kwargs):
         o_proj_block_size=globs.o_proj_block_size,
         router_bias=globs.router_bias,
         predictor_weights=None if globs.predictor_weights is None else _flatten_depth(globs.predictor_weights),
-        stream=torch.cuda.current_stream(globs.hidden_states.device),
+        stream=(torch.cuda.current_stream(globs.hidden_states.device)
+                if globs.hidden_states.device.type == "cuda" else None),
     )
     kwargs.update(launch_kwargs)
 

@@ -86,6 +86,12 @@ def _wait_and_arrive(words, d: ProtocolDims):
     return None, None, (MK_ERR_BAD_OPCODE, 0, 0, op)
 
 
+def _as_numpy(a) -> np.ndarray:
+    if hasattr(a, "detach"):  # torch tensor, possibly on a GPU
+        return a.detach().cpu().numpy()
+    return np.asarray(a)
+
+
 def simulate(instructions, barriers, dims: ProtocolDims) -> np.ndarray:
     """Replay the queues; return the final barrier tensor (a copy).
 
@@ -95,8 +101,8 @@ def simulate(instructions, barriers, dims: ProtocolDims) -> np.ndarray:
     its worker reaches it, or -- when no worker can progress -- a time-out of
     the lowest-numbered blocked worker.
     """
-    ins = np.asarray(instructions, dtype=np.int64)
-    bar = np.array(barriers, dtype=np.int64, copy=True)
+    ins = _as_numpy(instructions).astype(np.int64)
+    bar = _as_numpy(barriers).astype(np.int64, copy=True)
     W, Q, _ = ins.shape
     pos = [0] * W
     decoded = [[_wait_and_arrive(ins[w, q], dims) for q in range(Q)] for w in range(W)]

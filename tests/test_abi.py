@@ -1,0 +1,98 @@
+"""The C ABI boundary without a GPU: the library loads, exports every entry
+point include/*.h declares, the ctypes struct has the header's layout, and
+host-side validation rejects bad calls before any HIP call is made."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+import mk_mixtral
+from megakernels_amd.mixtral.mk import interpret_with_mk
+from megakernels_amd.mixtral.scheduler import make_globals
+from megakernels_amd.mixtral.synthetic import SMALL, make_synthetic_mixtral
+from megakernels_amd.scheduler import tensorize_instructions
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mk_mixtral.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not mk_mixtral.library_path().exists():
+        import __graft_entry__
+
+        __graft_entry__.build()
+    return mk_mixtral.load_library()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mk_mixtral_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "mk_mixtral_launch" in names
+    assert sorted(mk_mixtral.EXPORTED_SYMBOLS) == names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(mk_mixtral.library_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for name in declared_functions():
+        assert name in exported, name
+        assert hasattr(lib, name)
+
+
+def test_struct_layout_matches_header(tmp_path):
+    fields = [f for f, _ in mk_mixtral.MkMixtralGlobals._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "mk_mixtral.h"\nint main(void) {\n'
+        '  printf("sizeof %zu\\n", sizeof(mk_mixtral_globals));\n'
+        + "".join(f'  printf("{f} %zu\\n", offsetof(mk_mixtral_globals, {f}));\n' for f in fields)
+        + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    lines = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True)
+                 .stdout.splitlines())
+    assert int(lines.pop("sizeof")) == ctypes.sizeof(mk_mixtral.MkMixtralGlobals)
+    for f in fields:
+        assert int(lines[f]) == getattr(mk_mixtral.MkMixtralGlobals, f).offset, f
+
+
+def test_version_and_error_strings(lib):
+    assert lib.mk_mixtral_abi_version() == mk_mixtral.ABI_VERSION
+    for code in (0, 1, 2, 3, 4, 16, 17, 18, 19):
+        assert lib.mk_mixtral_error_string(code)
+    assert b"unknown" in lib.mk_mixtral_error_string(12345)
+
+
+def test_launch_validation_needs_no_gpu(lib):
+    # a null struct and a struct of the wrong ABI are rejected before any HIP call
+    assert lib.mk_mixtral_launch(None, None) == 1
+    g = mk_mixtral.MkMixtralGlobals()
+    g.struct_size = ctypes.sizeof(g)
+    g.abi_version = 99
+    assert lib.mk_mixtral_launch(ctypes.byref(g), None) == 1
+    g.abi_version = mk_mixtral.ABI_VERSION
+    assert lib.mk_mixtral_launch(ctypes.byref(g), None) == 1  # null tensors
+
+
+def test_python_launcher_rejects_bad_arguments():
+    model = make_synthetic_mixtral(SMALL, "cpu", 0)
+    g = make_globals(model, sm_count=2)
+    tensorize_instructions(g, [[], []])
+    with pytest.raises(ValueError, match="GPU"):
+        interpret_with_mk(g, mk_mixtral.mk_mixtral)
+    with pytest.raises(TypeError):
+        mk_mixtral.mk_mixtral(1, 2, 3)
+    # hidden_states on the CPU: refused before the library is called
+    args = [torch.empty(0)] * 17 + [torch.empty(4, dtype=torch.bfloat16)] + [torch.empty(0)] * 10
+    with pytest.raises(ValueError, match="GPU"):
+        mk_mixtral.build_globals_struct(*args, 0, 1.0, 1e-5, False)
