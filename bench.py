@@ -36,6 +36,11 @@ for p in (ROOT / "epic-kernel_amd", ROOT):
 
 METRIC = "batch-1 decode tokens/s, Mixtral-8x7B shape; MoE layer µs; % HBM peak"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes moved per launch of mk_mixtral_kernel at config 2: rocprofv3
+# FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the same counter
+# reads for a device copy of known size (FETCH x 2.0, WRITE x 1.0); the
+# counter runs are summarised under profiles/.
+MEASURED_TRAFFIC_BYTES = {"c2": 707_411_737}
 
 
 def moe_layer_bytes(cfg) -> int:
@@ -58,7 +63,7 @@ def cpu_model_name() -> str:
 class MoEBench:
     """Per-token launches of the MoE-only schedule over resident inputs."""
 
-    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, static_partition: bool = False):
+    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, work_sharing: bool = False):
         import torch
 
         import mk_mixtral
@@ -92,7 +97,7 @@ class MoEBench:
             kw.pop("stream", None)
             captured["g"] = mk_mixtral.build_globals_struct(*args, **kw)
 
-        interpret_with_mk(g, capture, static_partition=static_partition)
+        interpret_with_mk(g, capture, work_sharing=work_sharing)
         self.struct = captured["g"]
         self.lib = mk_mixtral.load_library()
         self.mk = mk_mixtral
@@ -221,22 +226,35 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--static-partition", action="store_true",
-                    help="each instruction processes only its own rows (no work sharing)")
+    ap.add_argument("--work-sharing", action="store_true",
+                    help="idle workers take unclaimed opcode-5 rows of other workers")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (reads MIB, writes MIB) and exit; "
+                         "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU design is described in DESIGN.md and is not benchmarked", file=sys.stderr)
+              "the expert/tensor-parallel split is a design, not a benchmarked path", file=sys.stderr)
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return
 
     from megakernels_amd.mixtral.synthetic import C1, C2
 
     cfg = C2 if args.config == "c2" else C1
     print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
-    bench = MoEBench(cfg, args.tokens, seed=0, static_partition=args.static_partition)
+    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing)
     timed = run_timed(bench, args.steps, args.warmup)
     dist = bench.per_launch_us(256)
     nbytes = moe_layer_bytes(cfg)
@@ -246,7 +264,7 @@ def main():
 
     skewed = None
     if not args.no_skewed:
-        sk = MoEBench(cfg, args.tokens, seed=0, static_partition=args.static_partition,
+        sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing,
                       router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
         sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
         sk_us = sk_timed["us_per_launch_events"]
@@ -285,7 +303,7 @@ def main():
             "workers": g.sm_count(),
             "expert_proj_block_size": g.expert_proj_block_size,
             "down_proj_block_size": g.down_proj_block_size,
-            "work_sharing": not args.static_partition,
+            "work_sharing": args.work_sharing,
         },
         "moe_layer_us": us,
         "moe_layer_us_per_launch": dist,
@@ -296,7 +314,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "bytes_per_launch": nbytes,
             "kernel": "mk_mixtral_kernel",
         },

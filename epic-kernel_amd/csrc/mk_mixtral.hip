@@ -1224,7 +1224,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const uint64_t ticks = us * kTicksPerUs;
     kp.timeout_ticks = ticks > 0xffffffffu ? 0xffffffffu : (uint32_t)ticks;
     kp.scratch = st->scratch;
-    kp.work_sharing = g->static_partition ? 0 : 1;
+    kp.work_sharing = g->work_sharing ? 1 : 0;
 
     if (e8)
         hipLaunchKernelGGL(mk_mixtral_kernel<8>, dim3((unsigned)g->num_workers), dim3(kThreads), lds,

@@ -20,9 +20,11 @@ sizes are the compile-time 16):
     bound on every in-kernel barrier wait (default 2 s);
 ``record_timings``
     write per-instruction ``s_memrealtime`` stamps into ``timings``;
-``static_partition``
-    process exactly each instruction's own rows (no work sharing between
-    workers; results and barrier counts are the same either way);
+``work_sharing``
+    let workers that finish their own opcode-5 rows take unclaimed rows of
+    other workers' opcode-5 instructions (default off: each instruction
+    processes exactly its own rows; results and barrier counts are the same
+    either way);
 ``debug_sync``
     synchronise after the launch and raise :class:`MKDeviceError` if the
     kernel recorded a failure.
@@ -145,7 +147,7 @@ class MkMixtralGlobals(ctypes.Structure):
         ("status", _P),
         ("spin_timeout_us", ctypes.c_uint32),
         ("record_timings", ctypes.c_int32),
-        ("static_partition", ctypes.c_int32),
+        ("work_sharing", ctypes.c_int32),
     ]
 
 
@@ -291,7 +293,7 @@ def build_globals_struct(
     status=None,
     spin_timeout_us: int = 0,
     record_timings: bool = False,
-    static_partition: bool = False,
+    work_sharing: bool = False,
 ) -> MkMixtralGlobals:
     """Validate the reference-ordered arguments and fill the C struct.
 
@@ -388,7 +390,7 @@ def build_globals_struct(
     g.status = None if status is None else status.data_ptr()
     g.spin_timeout_us = int(spin_timeout_us)
     g.record_timings = int(bool(record_timings))
-    g.static_partition = int(bool(static_partition))
+    g.work_sharing = int(bool(work_sharing))
     return g
 
 

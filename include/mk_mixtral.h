@@ -168,8 +168,8 @@ typedef struct mk_mixtral_globals {
     int32_t *status;               /* device int32[16], NULL = library-owned buffer */
     uint32_t spin_timeout_us;      /* barrier spin limit, 0 = 2 s            */
     int32_t record_timings;        /* nonzero: write timing slots           */
-    int32_t static_partition;      /* nonzero: each instruction does exactly its
-                                      own rows; zero: idle workers also take
+    int32_t work_sharing;          /* zero: each instruction does exactly its
+                                      own rows; nonzero: idle workers also take
                                       unclaimed rows of other opcode-5
                                       instructions of the same layer (same
                                       results, same barrier counts) */

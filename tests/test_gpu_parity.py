@@ -144,3 +144,14 @@ def test_c2_tokens():
         res = case.run_token(x)
         _report("c2", res)
         res.assert_ok()
+
+
+@pytest.mark.parametrize("config", ["c1", "small"])
+def test_work_sharing(config):
+    """Cross-worker sharing of opcode-5 rows: same results and barrier
+    counts as the static partition."""
+    cfg = C1 if config == "c1" else SMALL
+    case = MoECase(cfg, seed=13)
+    for x in draw_tokens(case.cpu_model, 3):
+        res = case.run_token(x, work_sharing=True)
+        res.assert_ok()
