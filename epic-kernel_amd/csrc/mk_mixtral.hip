@@ -32,8 +32,8 @@
 // [512c + 8l, 512c + 8l + 8) of chunk c, so one wave-wide dwordx4 load reads
 // 1 KiB of contiguous weights.  Weights go HBM -> VGPR with non-temporal
 // loads; the activation vector is staged once per instruction in LDS; each
-// 8-element product uses v_dot2 (bf16 pairs, fp32 accumulate); the row sum
-// is a 64-lane butterfly.
+// bf16 pair is widened exactly to fp32 and fused-multiply-added into an fp32
+// accumulator; the row sum is a 64-lane DPP reduction.
 
 #include <hip/hip_runtime.h>
 
