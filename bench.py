@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the same counter
 # reads for a device copy of known size (FETCH x 2.0, WRITE x 1.0); the
 # counter runs are summarised under profiles/.
-MEASURED_TRAFFIC_BYTES = {"c2": 707_411_737}
+MEASURED_TRAFFIC_BYTES = {"c2": 708_573_701}
 
 
 def moe_layer_bytes(cfg) -> int:
@@ -63,7 +63,8 @@ def cpu_model_name() -> str:
 class MoEBench:
     """Per-token launches of the MoE-only schedule over resident inputs."""
 
-    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, work_sharing: bool = False):
+    def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, work_sharing: bool = False,
+                 balance: bool = False, calib_tokens: int = 16):
         import torch
 
         import mk_mixtral
@@ -77,10 +78,13 @@ class MoEBench:
         self.tokens = tokens
         self.model = make_synthetic_mixtral(cfg, self.dev, seed, router_bias=router_bias)
         self.residuals = make_residuals(tokens, cfg.hidden_size, generator=self.model.generator)
-        self.globs = g = make_globals(self.model)
+        # speed-balanced partitions need row-granular blocks
+        bs = dict(expert_proj_block_size=1, down_proj_block_size=1) if balance else {}
+        self.globs = g = make_globals(self.model, **bs)
         nodes, end = make_moe_dag(g)
         self.schedule = Schedule(g, nodes, end)
-        tensorize_instructions(g, assign_to_sms("rr", schedule=self.schedule))
+        self.queues = assign_to_sms("rr", schedule=self.schedule)
+        tensorize_instructions(g, self.queues)
         # one barrier tensor and one residual row per token, so a step needs
         # no per-token resets between launches
         bars = torch.zeros([tokens, *g.barriers.shape], dtype=torch.int32, device=self.dev)
@@ -103,6 +107,45 @@ class MoEBench:
         self.mk = mk_mixtral
         self.row_bytes = self.work.stride(0) * 2
         self.bar_bytes = self.bars.stride(0) * 4
+        self.weights = None
+        if balance:
+            self.calibrate(calib_tokens)
+
+    def calibrate(self, n: int):
+        """Measure each worker's opcode-5 streaming rate on `n` launches (timing
+        record on), then re-split the opcode-5/6 rows by speed."""
+        import numpy as np
+
+        from megakernels_amd.mixtral.balance import rebalance_queues, weights_from_rates, worker_rates_from_timings
+        from megakernels_amd.scheduler import tensorize_instructions
+
+        torch, g, s = self.torch, self.globs, self.struct
+        s.record_timings = 1
+        s.timings = g.timings.data_ptr()
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        self.work.copy_(self.residuals)
+        self.bars.copy_(self.bars_init)
+        rates = []
+        for t in range(n + 2):
+            self._launch(t % self.tokens, stream)
+            torch.cuda.synchronize()
+            if t >= 2:  # first launches warm up
+                rates.append(worker_rates_from_timings(g.timings, g.instructions, g.expert_proj_block_size))
+        self.check_status()
+        self.weights = weights_from_rates(np.nanmean(np.stack(rates), axis=0))
+        self.queues = rebalance_queues(self.queues, g, self.weights)
+        tensorize_instructions(g, self.queues)
+        s.instructions = g.instructions.data_ptr()
+        s.queue_len = g.instructions.shape[1]
+        s.record_timings = 0
+        s.timings = g.timings.data_ptr()
+
+    def linear_instructions(self):
+        """The launched instructions in topological order (round-robin
+        assignment: linear index i sits at queue i % W, position i // W)."""
+        W = len(self.queues)
+        n = len(self.schedule.get_linear_instructions())
+        return [self.queues[i % W][i // W] for i in range(n)]
 
     def _launch(self, t: int, stream_ptr):
         s = self.struct
@@ -172,8 +215,10 @@ def cpu_baseline(bench, seconds: float, threads: int):
 
     oracle.set_num_threads(threads)
     cpu_model = to_device(bench.model, "cpu")
-    g = make_globals(cpu_model, sm_count=bench.globs.sm_count())
-    linear = bench.schedule.get_linear_instructions()
+    g = make_globals(cpu_model, sm_count=bench.globs.sm_count(),
+                     expert_proj_block_size=bench.globs.expert_proj_block_size,
+                     down_proj_block_size=bench.globs.down_proj_block_size)
+    linear = bench.linear_instructions()
     residuals = bench.residuals.cpu()
     done = 0
     agree = 0
@@ -226,6 +271,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--balance", action="store_true",
+                    help="re-split rows by per-worker speed measured on a few launches (block size 1)")
     ap.add_argument("--work-sharing", action="store_true",
                     help="idle workers take unclaimed opcode-5 rows of other workers")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -254,7 +301,7 @@ def main():
 
     cfg = C2 if args.config == "c2" else C1
     print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
-    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing)
+    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance)
     timed = run_timed(bench, args.steps, args.warmup)
     dist = bench.per_launch_us(256)
     nbytes = moe_layer_bytes(cfg)
@@ -264,7 +311,7 @@ def main():
 
     skewed = None
     if not args.no_skewed:
-        sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing,
+        sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
                       router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
         sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
         sk_us = sk_timed["us_per_launch_events"]
@@ -304,6 +351,7 @@ def main():
             "expert_proj_block_size": g.expert_proj_block_size,
             "down_proj_block_size": g.down_proj_block_size,
             "work_sharing": args.work_sharing,
+            "speed_balanced_partition": args.balance,
         },
         "moe_layer_us": us,
         "moe_layer_us_per_launch": dist,

@@ -53,10 +53,15 @@
 #ifndef MK_DOT2_BUILTIN
 #define MK_DOT2_BUILTIN 0
 #endif
-// Items at the end of each opcode-5 instruction that are claimed through its
-// cursor (and so can be taken by other workers); the rest run statically.
+// Work sharing (opcode 5): the last MK_TAIL_ITEMS items of every opcode-5
+// instruction are claimed through a cursor in HBM, so the other workers of
+// its group (MK_POOL_GROUP consecutive workers, which sit on different XCDs)
+// can take them once their own instruction is done.
 #ifndef MK_TAIL_ITEMS
-#define MK_TAIL_ITEMS 32
+#define MK_TAIL_ITEMS 16
+#endif
+#ifndef MK_POOL_GROUP
+#define MK_POOL_GROUP 8
 #endif
 // Spin back-off: a waiting workgroup polls its counter every ~64 * N clocks,
 // N growing from 1 to MK_SPIN_SLEEP_MAX, so hundreds of idle workgroups do not
@@ -66,6 +71,10 @@
 #endif
 #ifndef MK_CLAIM_LOOKAHEAD
 #define MK_CLAIM_LOOKAHEAD 1
+#endif
+// Opcode-6 cache warming while waiting for opcode 5: items per wave (0 = off).
+#ifndef MK_PF_ROUNDS
+#define MK_PF_ROUNDS 1
 #endif
 
 namespace {
@@ -80,8 +89,10 @@ constexpr uint32_t kTicksPerUs = 100;  // s_memrealtime runs at 100 MHz
 constexpr int kCachePolicySc1 = 16;     // buffer-load cache policy: device scope
 // Work-sharing scratch (int32): [0] exit counter, then a (cursor, done) pair
 // per instruction slot w * queue_len + q.
-constexpr int kScratchJobBase = 16;
-constexpr int kMaxHelpCandidates = 1024;
+constexpr int kScratchSlotBase = 16;
+constexpr int kPoolGroup = MK_POOL_GROUP;
+constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) that can be shared
+static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
 constexpr int kRowBatchLds = 64;  // rows per opcode-6 batch (partial sums in LDS)
 constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 16 * 512)
 
@@ -127,11 +138,13 @@ struct SharedState {
     int route_idx[2];
     float route_score[2];  // bf16 score values widened to fp32
     int flag;
-    int dbg_own, dbg_help, dbg_rounds;  // work-sharing counters for the timing record
-    int next_item;                      // per-instruction item counter shared by the waves
+    int next_item;  // per-instruction item counter shared by the waves
     float part[kRowBatchLds * 2 * kMaxSegments];  // opcode-6 partial sums: [row][slot][segment]
-    int ncand;
-    int cand[kMaxHelpCandidates];
+    // opcode-5 instructions of this worker's group for the current layer, in
+    // (worker, slot) order: instruction slot, first FFN row, rows
+    int pool_n;
+    int wave_cnt[kWaves];
+    int pool_slot[kMaxPoolIns], pool_row0[kMaxPoolIns], pool_nrows[kMaxPoolIns];
 };
 
 struct Ctx {
@@ -273,9 +286,9 @@ __device__ __forceinline__ bool aborted(const KParams &p) {
     return __hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// Record the first failure (thread 0 of the reporting workgroup only).
-__device__ void report_error(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected, int seen) {
-    if (threadIdx.x != 0) return;
+// Record the first failure; called by one lane.
+__device__ void report_error_lane(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected,
+                                  int seen) {
     int zero = 0;
     if (__hip_atomic_compare_exchange_strong(p.status, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT)) {
@@ -286,6 +299,11 @@ __device__ void report_error(const KParams &p, int code, const Ctx &c, int opcod
         p.status[MK_STATUS_EXPECTED] = expected;
         p.status[MK_STATUS_SEEN] = seen;
     }
+}
+
+// Record the first failure (thread 0 of the reporting workgroup only).
+__device__ void report_error(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected, int seen) {
+    if (threadIdx.x == 0) report_error_lane(p, code, c, opcode, layer, expected, seen);
 }
 
 // Wait until *ctr >= expected.  Thread 0 spins; the result is broadcast.
@@ -332,6 +350,7 @@ __device__ __forceinline__ void drain_and_sync() {
 __device__ __forceinline__ void arrive(int32_t *ctr, int n) {
     if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
 
 // ---------------------------------------------------------------------------
 // GEMV core: two rows at once, N chunks of 512 columns each
@@ -574,6 +593,58 @@ __device__ __forceinline__ int claim_issue(int32_t *cursor, int lane) {
     return v;
 }
 
+// Collect the group's opcode-5 instructions of `layer` (all queue slots of
+// workers [group * kPoolGroup, +kPoolGroup)) into sh.pool_*, in (worker,
+// slot) order, so every member enumerates the pooled items identically.
+// Instructions with out-of-range operands are left out (their owner reports
+// them).  Ends with a workgroup barrier.
+__device__ void pool_scan(const KParams &p, SharedState &sh, int layer, int group) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int w0 = group * kPoolGroup;
+    const int w1 = min((int)gridDim.x, w0 + kPoolGroup);
+    const int n = (w1 - w0) * p.queue_len;
+    if (tid == 0) sh.pool_n = 0;
+    __syncthreads();
+    for (int base = 0; base < n; base += kThreads) {
+        const int i = base + tid;
+        bool m = false;
+        int start = 0, nb = 0;
+        if (i < n) {
+            const int32_t *ins = p.instructions + ((size_t)w0 * p.queue_len + i) * MK_INTS_PER_INSTRUCTION;
+            start = ins[2];
+            nb = ins[3];
+            m = ins[0] == 5 && ins[1] == layer && start >= 0 && nb > 0 &&
+                (int64_t)(start + nb) * p.expert_bs <= (int64_t)p.F;
+        }
+        const uint64_t bal = __ballot(m);
+        if (lane == 0) sh.wave_cnt[wave] = __popcll(bal);
+        __syncthreads();
+        int off = sh.pool_n;
+        for (int v = 0; v < wave; ++v) off += sh.wave_cnt[v];
+        if (m) {
+            const int k = off + __popcll(bal & ((1ull << lane) - 1ull));
+            if (k < kMaxPoolIns) {
+                sh.pool_slot[k] = w0 * p.queue_len + i;
+                sh.pool_row0[k] = start * p.expert_bs;
+                sh.pool_nrows[k] = nb * p.expert_bs;
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int tot = 0;
+            for (int v = 0; v < kWaves; ++v) tot += sh.wave_cnt[v];
+            sh.pool_n += tot;
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ int tail_items(int items) { return items < MK_TAIL_ITEMS ? items : MK_TAIL_ITEMS; }
+
+__device__ __forceinline__ int32_t *slot_cursor(const KParams &p, int slot) {
+    return p.scratch + kScratchSlotBase + 2 * slot;
+}
+
 // Items [first, first + count) of an opcode-5 instruction whose FFN rows
 // start at row0 (nrows rows, items 0 .. 2*nrows), claimed one at a time from
 // the instruction's cursor (the next claim is issued before the current
@@ -583,7 +654,6 @@ __device__ int upgate_claimed(const KParams &p, const u32x4 *act, int layer, int
     int done_here = 0;
     int c = __builtin_amdgcn_readfirstlane(claim_issue(cursor, lane));
     while (c < count) {
-#if MK_CLAIM_LOOKAHEAD
         int next_raw = claim_issue(cursor, lane);
         upgate_item(p, act, layer, row0, nrows, e0, e1, first + c, lane);
         ++done_here;
@@ -591,66 +661,52 @@ __device__ int upgate_claimed(const KParams &p, const u32x4 *act, int layer, int
         // broadcast (and the wait for the atomic) above the item's loads
         asm volatile("" : "+v"(next_raw));
         c = __builtin_amdgcn_readfirstlane(next_raw);
-#else
-        upgate_item(p, act, layer, row0, nrows, e0, e1, first + c, lane);
-        ++done_here;
-        c = __builtin_amdgcn_readfirstlane(claim_issue(cursor, lane));
-#endif
     }
     return done_here;
 }
 
-// Publish `n` finished items of an instruction after this wave's (coherent)
-// stores have completed.
-__device__ __forceinline__ void publish_done(int32_t *done, int n, int lane) {
+// A wave reports `n` finished items of an instruction (after its own stores
+// have completed).  The owner's report carries one extra count, so an
+// instruction completes only after its owner has also published the routing
+// (for the block-0 instruction); the report that reaches items + 1 arrives
+// for the instruction's rows on the layer and chunk counters.
+__device__ __forceinline__ void publish_items(const KParams &p, int32_t *done, int n, int items, int row0,
+                                              int nrows, int layer, int lane) {
     if (n <= 0) return;
     __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) __hip_atomic_fetch_add(done, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+        const int prev = __hip_atomic_fetch_add(done, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev + n == items + 1)
+            __hip_atomic_fetch_add(bar_at(p, layer, 5), nrows / p.expert_bs, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
-__device__ __forceinline__ int tail_items(int items) { return items < MK_TAIL_ITEMS ? items : MK_TAIL_ITEMS; }
-
-// After its own instruction, a workgroup helps the other opcode-5
-// instructions of the same layer (any worker, any queue slot) whose claimable
-// tails still have items.  It works in rounds: one parallel pass over the
-// instruction table reads every candidate's cursor (one round trip), then all
-// waves claim from one candidate picked by workgroup index, so helpers spread
-// over the unfinished instructions.  Routing is a deterministic function of
-// the layer's inputs, so the helper's experts are the owner's.
-__device__ void help_upgate(const KParams &p, SharedState &sh, const u32x4 *act, int layer, int self_slot, int e0,
-                            int e1) {
-    if (threadIdx.x == 0) sh.dbg_rounds = 0;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int total = (int)gridDim.x * p.queue_len;
-    for (int round = 0; round < kMaxHelpCandidates; ++round) {
-        if (tid == 0) sh.ncand = 0;
-        __syncthreads();
-        for (int sl = tid; sl < total; sl += kThreads) {
-            const int32_t *ins = p.instructions + (size_t)sl * MK_INTS_PER_INSTRUCTION;
-            if (sl == self_slot || ins[0] != 5 || ins[1] != layer) continue;
-            const int start = ins[2], nb = ins[3];
-            if (start < 0 || nb <= 0 || (int64_t)(start + nb) * p.expert_bs > (int64_t)p.F) continue;
-            const int tail = tail_items(2 * nb * p.expert_bs);
-            if ((int)ld_dev32(p.scratch + kScratchJobBase + 2 * sl) >= tail) continue;
-            const int k = atomicAdd(&sh.ncand, 1);
-            if (k < kMaxHelpCandidates) sh.cand[k] = sl;
+// After its own instruction, each wave takes unclaimed tail items of the
+// other group instructions: one vector load reads every cursor, the wave
+// picks the first instruction with items left (starting at an offset that
+// spreads the waves), claims from it until it is exhausted, and repeats.
+// Routing is a function of the layer's inputs only, so the experts are the
+// owner's.
+__device__ void steal_upgate(const KParams &p, const SharedState &sh, const u32x4 *act, int layer, int self_k,
+                             int e0, int e1, int lane, int wave) {
+    const int n = sh.pool_n;
+    const int start = (self_k + 1 + wave) % n;
+    for (;;) {
+        int left = 0;
+        if (lane < n && lane != self_k) {
+            const int tail = tail_items(2 * sh.pool_nrows[lane]);
+            left = tail - (int)ld_dev32(slot_cursor(p, sh.pool_slot[lane]));
         }
-        __syncthreads();
-        const int n = min(sh.ncand, kMaxHelpCandidates);
-        if (n == 0) break;
-        const int sl = __builtin_amdgcn_readfirstlane(sh.cand[((int)blockIdx.x + round) % n]);
-        const int32_t *ins = p.instructions + (size_t)sl * MK_INTS_PER_INSTRUCTION;
-        const int start = __builtin_amdgcn_readfirstlane(ins[2]);
-        const int nb = __builtin_amdgcn_readfirstlane(ins[3]);
-        const int items = 2 * nb * p.expert_bs;
-        const int tail = tail_items(items);
-        int32_t *cursor = p.scratch + kScratchJobBase + 2 * sl;
-        const int n_done = upgate_claimed(p, act, layer, start * p.expert_bs, nb * p.expert_bs, e0, e1,
-                                          items - tail, tail, cursor, lane);
-        publish_done(cursor + 1, n_done, lane);
-        if (lane == 0 && n_done) atomicAdd(&sh.dbg_help, n_done);
-        if (tid == 0) sh.dbg_rounds = round + 1;
-        __syncthreads();
+        uint64_t b = __ballot(left > 0);
+        if (b == 0) break;
+        // first candidate at or after `start`, wrapping around
+        const uint64_t hi = b >> start;
+        const int v = hi != 0 ? start + (int)__builtin_ctzll(hi) : (int)__builtin_ctzll(b);
+        const int nrows = sh.pool_nrows[v], items = 2 * nrows, tail = tail_items(items);
+        int32_t *cursor = slot_cursor(p, sh.pool_slot[v]);
+        const int got = upgate_claimed(p, act, layer, sh.pool_row0[v], nrows, e0, e1, items - tail, tail, cursor, lane);
+        publish_items(p, cursor + 1, got, items, sh.pool_row0[v], nrows, layer, lane);
     }
 }
 
@@ -665,11 +721,15 @@ __device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *a
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 5, layer, start, nb);
         return false;
     }
+    // an empty instruction owns no rows (another one starts at block 0)
+    if (nb == 0) return true;
     RouterRegs<kE> rr;
     router_prefetch<kE>(p, sh, layer, p.router, rr);
     // items 0 .. kWaves-1 go to waves 0 .. kWaves-1, the rest through the
     // LDS counter (reset here; the wait below is a workgroup barrier)
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    // the pool's instruction list does not depend on the producers either
+    if (p.work_sharing) pool_scan(p, sh, layer, c.worker / kPoolGroup);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
@@ -703,37 +763,28 @@ __device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *a
 
     const int lane = tid & 63, wave = tid >> 6;
     const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
-    if (p.work_sharing) {
+    if (p.work_sharing && sh.pool_n <= kMaxPoolIns) {
+        // Own items first: all but the tail from the LDS counter, the tail
+        // through this instruction's cursor; then the group's leftovers.  No
+        // worker waits for another: whoever completes an instruction's items
+        // arrives for it.
         const int self_slot = c.worker * p.queue_len + c.slot;
-        int32_t *cursor = p.scratch + kScratchJobBase + 2 * self_slot;
-        const int items = 2 * nrows;
-        const int tail = tail_items(items);
-        if (tid == 0) {
-            sh.dbg_own = 0;
-            sh.dbg_help = 0;
-        }
-        __syncthreads();
-        int n_done = 0;
+        int self_k = 0;
+        while (self_k < sh.pool_n - 1 && sh.pool_slot[self_k] != self_slot) ++self_k;
+        int32_t *cursor = slot_cursor(p, self_slot);
+        const int items = 2 * nrows, tail = tail_items(items);
+        int mine = 0;
         for (int it = wave; it < items - tail; it = next_local_item(sh, lane)) {
             upgate_item(p, act, layer, row0, nrows, t.i0, t.i1, it, lane);
-            ++n_done;
+            ++mine;
         }
-        n_done += upgate_claimed(p, act, layer, row0, nrows, t.i0, t.i1, items - tail, tail, cursor, lane);
-        publish_done(cursor + 1, n_done, lane);
-        if (lane == 0) atomicAdd(&sh.dbg_own, n_done);
-        __syncthreads();
-        // items taken by helpers must be finished before this instruction arrives
-        if (!wait_ge(p, sh, cursor + 1, items, c, 5, layer)) return false;
-        arrive(bar_at(p, layer, 5), nb);
+        mine += upgate_claimed(p, act, layer, row0, nrows, t.i0, t.i1, items - tail, tail, cursor, lane);
+        // wave 0 also carries the owner's extra count
+        publish_items(p, cursor + 1, mine + (wave == 0), items, row0, nrows, layer, lane);
+        stamp(tim, MK_TEVENT_AT_GMEM_STORE);
+        if (sh.pool_n > 1) steal_upgate(p, sh, act, layer, self_k, t.i0, t.i1, lane, wave);
+        drain_and_sync();
         stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
-        help_upgate(p, sh, act, layer, self_slot, t.i0, t.i1);
-        __syncthreads();
-        if (tim != nullptr && tid == 0) {
-            tim[56] = sh.dbg_own;
-            tim[57] = sh.dbg_help;
-            tim[58] = sh.dbg_rounds;
-        }
-        stamp(tim, 59);
     } else {
         // Waves take items from a workgroup counter in LDS rather than a
         // fixed stride: the memory pipeline favours older waves, so with a
@@ -752,6 +803,12 @@ __device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *a
         stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     }
     return true;
+}
+
+// Byte offset in the dynamic LDS of the 8 KiB (1 KiB per wave) that the
+// opcode-6 cache warming writes into: after the SiLU staging area.
+__device__ __forceinline__ uint32_t lds_prefetch_offset(const KParams &p) {
+    return (uint32_t)p.F * 4u;
 }
 
 // ---------------------------------------------------------------------------
@@ -847,7 +904,38 @@ __device__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act
     }
 
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
+    int32_t *ready = bar_at(p, layer, 5);
+    const int expected = p.F / p.expert_bs;
+#if MK_PF_ROUNDS > 0
+    // Cache warming: if opcode 5 is still running elsewhere, HBM has spare
+    // bandwidth, so each wave reads the rows of its next items once more
+    // with ordinary (cache-allocating) loads straight into a scratch corner
+    // of LDS; after the wait, their regular loads find them in the
+    // Infinity Cache.  Workgroups that arrive after the last producer skip
+    // it.
+    if (known) {
+        if (tid == 0) sh.flag = (int)ld_dev32(ready) < expected;
+        __syncthreads();
+        const bool warm = sh.flag != 0;
+        __syncthreads();
+        if (warm) {
+            __attribute__((address_space(3))) void *sink =
+                (__attribute__((address_space(3))) void *)(act + (lds_prefetch_offset(p) >> 4) + wave * 64);
+            for (int m = 1; m <= MK_PF_ROUNDS; ++m) {
+                const int it = wave + m * kWaves;
+                if (it >= first_batch * 2 * S) break;
+                const DownItem d = down_item(it, S, nc);
+                const int e = sh.route_idx[d.slot];
+                const uint16_t *row = p.down + ((size_t)(layer * p.E + e) * p.H + row0 + d.row) * (size_t)p.F;
+                const u32x4 *w = reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane;
+                for (int i = 0; i < d.n; ++i)
+                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(w + i * 64),
+                                                     sink, 16, 0, 0);
+            }
+        }
+    }
+#endif
+    if (!wait_ge(p, sh, ready, expected, c, 6, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
     int e0, e1;
@@ -1002,7 +1090,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     __syncthreads();
     if (sh.flag) {
         const int n = 2 * (int)gridDim.x * p.queue_len;
-        for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchJobBase + i] = 0;
+        for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
         drain_and_sync();
         if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1072,7 +1160,8 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 size_t lds_bytes_for(const mk_mixtral_globals *g) {
     const size_t normed = (size_t)g->hidden_size * 2;
-    const size_t silu = (size_t)g->intermediate_size * 2 * 2;
+    // both SiLU rows, then the opcode-6 cache-warming sink (1 KiB per wave)
+    const size_t silu = (size_t)g->intermediate_size * 2 * 2 + (size_t)kWaves * 1024;
     size_t need = normed > silu ? normed : silu;
     return need > (size_t)kMinLdsBytes ? need : (size_t)kMinLdsBytes;
 }
@@ -1170,8 +1259,8 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (g->num_workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
 
-    // work-sharing counters: exit counter + (cursor, done) per instruction slot
-    const size_t need = kScratchJobBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len;
+    // exit counter and work-sharing (cursor, done) per instruction slot
+    const size_t need = kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len;
     if (need > st->scratch_ints) {
         std::lock_guard<std::mutex> lock(g_mutex);
         if (need > st->scratch_ints) {

@@ -95,7 +95,7 @@ class MoECase:
 
     def __init__(self, config, seed=0, device="cuda", workers=None, ln_weight_std=None, router_bias=None,
                  predictor_sigma=None, expert_proj_block_size=None, down_proj_block_size=None,
-                 predict=False, mode="rr", generate_on_device=False, stop_after_op=None):
+                 predict=False, mode="rr", generate_on_device=False, stop_after_op=None, worker_weights=None):
         dev = torch.device(device)
         gen_dev = dev if generate_on_device else torch.device("cpu")
         model = make_synthetic_mixtral(config, gen_dev, seed, ln_weight_std=ln_weight_std,
@@ -117,7 +117,13 @@ class MoECase:
         self.g_cpu = make_globals(self.cpu_model, **kw)
         nodes, end = make_moe_dag(self.g_gpu, predict=predict, stop_after_op=stop_after_op)
         self.schedule = Schedule(self.g_gpu, nodes, end)
-        tensorize_instructions(self.g_gpu, assign_to_sms(mode, schedule=self.schedule))
+        queues = assign_to_sms(mode, schedule=self.schedule)
+        if worker_weights is not None:
+            from megakernels_amd.mixtral.balance import rebalance_queues
+
+            # the oracle keeps the even partition: results do not depend on it
+            queues = rebalance_queues(queues, self.g_gpu, worker_weights)
+        tensorize_instructions(self.g_gpu, queues)
         self.linear = self.schedule.get_linear_instructions()
         self.stop_after_op = stop_after_op
 

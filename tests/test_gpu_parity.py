@@ -146,12 +146,26 @@ def test_c2_tokens():
         res.assert_ok()
 
 
-@pytest.mark.parametrize("config", ["c1", "small"])
-def test_work_sharing(config):
-    """Cross-worker sharing of opcode-5 rows: same results and barrier
-    counts as the static partition."""
+@pytest.mark.parametrize("config,workers,mode", [("c1", None, "rr"), ("small", None, "rr"), ("small", 7, "rr"),
+                                                 ("small", 1, "rr"), ("c1", None, "dag"), ("c1", 20, "zz")])
+def test_work_sharing(config, workers, mode):
+    """Pooled opcode-5 items (groups of consecutive workers share one claim
+    counter): same results and barrier counts as the static partition."""
     cfg = C1 if config == "c1" else SMALL
-    case = MoECase(cfg, seed=13)
+    case = MoECase(cfg, seed=13, workers=workers, mode=mode, predict=(mode == "dag"))
     for x in draw_tokens(case.cpu_model, 3):
         res = case.run_token(x, work_sharing=True)
         res.assert_ok()
+
+
+@pytest.mark.parametrize("config", ["c1", "small"])
+def test_speed_balanced_partition(config):
+    """Row partitions re-split by per-worker speed (odd XCDs slower), block
+    size 1: same results and barrier totals as the oracle's even partition."""
+    cfg = C1 if config == "c1" else SMALL
+    W = torch.cuda.get_device_properties(0).multi_processor_count
+    weights = [1.07 if w % 2 == 0 else 0.93 for w in range(W)]
+    case = MoECase(cfg, seed=17, expert_proj_block_size=1, down_proj_block_size=1, worker_weights=weights)
+    for x in draw_tokens(case.cpu_model, 3):
+        case.run_token(x).assert_ok()
+        case.run_token(x, work_sharing=True).assert_ok()
