@@ -204,6 +204,28 @@ def run_timed(bench, steps: int, warmup: int):
     return {"wall_s": wall, "gpu_s": gpu_s, "launches": launches, "us_per_launch_events": gpu_s / launches * 1e6}
 
 
+def record_trace(bench, path: str, launches: int = 8):
+    """Launch `launches` tokens with the timing record on (after the timed
+    region, so it does not perturb the measurement), save the last record."""
+    from megakernels_amd.trace import TimingRecord, format_report, save_record
+
+    torch, g, s = bench.torch, bench.globs, bench.struct
+    s.record_timings = 1
+    s.timings = g.timings.data_ptr()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(bench.dev).cuda_stream)
+    bench.work.copy_(bench.residuals)
+    bench.bars.copy_(bench.bars_init)
+    for t in range(launches):
+        g.timings.zero_()
+        bench._launch(t % bench.tokens, stream)
+    torch.cuda.synchronize()
+    bench.check_status()
+    s.record_timings = 0
+    rec = TimingRecord.from_globals(g)
+    save_record(path, rec)
+    print(format_report(rec), file=sys.stderr, flush=True)
+
+
 def cpu_baseline(bench, seconds: float, threads: int):
     """The CPU oracle (restated python_vm, C + OpenMP) on the same weights,
     inputs and instruction list, over a bounded sample of tokens."""
@@ -275,6 +297,9 @@ def main():
                     help="re-split rows by per-worker speed measured on a few launches (block size 1)")
     ap.add_argument("--work-sharing", action="store_true",
                     help="idle workers take unclaimed opcode-5 rows of other workers")
+    ap.add_argument("--trace", default="", metavar="NPZ",
+                    help="after the timed run, record the kernel's timing slots for 8 launches, save the "
+                         "last as NPZ and print the trace analysis to stderr")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (reads MIB, writes MIB) and exit; "
                          "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -304,6 +329,8 @@ def main():
     bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance)
     timed = run_timed(bench, args.steps, args.warmup)
     dist = bench.per_launch_us(256)
+    if args.trace:
+        record_trace(bench, args.trace)
     nbytes = moe_layer_bytes(cfg)
     us = timed["us_per_launch_events"]
     achieved = nbytes / (us * 1e-6) / 1e9

@@ -1,0 +1,86 @@
+"""Timing-record analysis (megakernels_amd/trace.py) on synthetic records
+whose answers are known in closed form."""
+
+import numpy as np
+import pytest
+
+from megakernels_amd.trace import (
+    TimingRecord,
+    barrier_waits,
+    format_report,
+    hbm_utilization,
+    load_record,
+    phase_summary,
+    save_record,
+)
+
+H, F, E = 512, 1024, 8
+
+
+def _record(t0=1000):
+    W, Q = 2, 2
+    ins = np.zeros((W, Q, 32), dtype=np.int32)
+    tim = np.zeros((W, Q, 128), dtype=np.int32)
+    ins[0, 0, :4] = [5, 0, 0, 4]        # 4 blocks of 8 rows
+    ins[1, 0, :4] = [5, 0, 4, 4]
+    ins[0, 1, :5] = [6, 0, 0, 16, 0]    # 16 blocks of 16 rows
+    ins[1, 1, :5] = [6, 0, 16, 32, 0]
+
+    def stamp(w, q, start, wait_at, wait_done, first, done, end):
+        for slot, us in ((0, start), (44, wait_at), (45, wait_done), (48, first), (47, done), (4, end)):
+            tim[w, q, slot] = np.uint32((t0 + int(round(us * 100))) & 0xFFFFFFFF).view(np.int32)
+
+    stamp(0, 0, 0, 0.5, 1.5, 2, 12, 12.5)
+    stamp(1, 0, 0.2, 0.7, 1.7, 2.2, 14.2, 14.5)
+    stamp(0, 1, 12.5, 12.6, 15.0, 15.5, 25.5, 26)
+    stamp(1, 1, 14.5, 14.6, 15.0, 15.5, 25.5, 26)
+    return TimingRecord(tim, ins, H, F, E, expert_proj_block_size=8, down_proj_block_size=16)
+
+
+def test_micros_relative_and_wrapping():
+    rec = _record()
+    t = rec.micros()
+    assert t[0, 0, 0] == 0.0 and t[1, 0, 0] == pytest.approx(0.2)
+    assert t[0, 1, 4] == pytest.approx(26.0)
+    assert np.isnan(t[0, 0, 100])  # never written
+    # the 32-bit clock wraps between the first and last stamps
+    wrapped = _record(t0=0xFFFFFFFF - 500)
+    assert np.allclose(np.nan_to_num(wrapped.micros()), np.nan_to_num(t))
+
+
+def test_barrier_waits():
+    bw = barrier_waits(_record())
+    op5, op6 = bw["by_opcode"][5], bw["by_opcode"][6]
+    assert op5["count"] == 2 and op5["wait_us"] == pytest.approx(2.0)
+    assert op6["wait_us"] == pytest.approx(2.4 + 0.4)
+    assert op5["instr_us"] == pytest.approx(12.5 + 14.3)
+    assert bw["by_layer"][0][6] == pytest.approx(2.8)
+
+
+def test_hbm_utilization_conserves_bytes():
+    rec = _record()
+    starts, gbs, frac, total = hbm_utilization(rec, bin_us=0.5, peak_gbs=1000.0)
+    b5 = 2 * 2 * 32 * H * 2
+    b6 = 2 * 256 * F * 2
+    assert rec.streamed_bytes(0, 0) == b5 and rec.streamed_bytes(1, 1) == b6
+    assert total == 2 * b5 + 2 * b6
+    # integral of the binned rate equals the bytes
+    assert np.sum(gbs) * 0.5 * 1e3 == pytest.approx(total, rel=1e-9)
+    assert np.allclose(frac, gbs / 1000.0)
+    # during 2.2 .. 12 us both opcode-5 instructions stream
+    i = int(5.0 / 0.5)
+    expect = (b5 / 10.0 + b5 / 12.0) / 1e3
+    assert gbs[i] == pytest.approx(expect)
+
+
+def test_phase_summary_and_report(tmp_path):
+    rec = _record()
+    ps = phase_summary(rec)
+    assert ps[("RmsRouterUpgate", "first_load")][0] == pytest.approx(2.0)
+    assert ps[("ExpertDownProjFused", "done")][-1] == pytest.approx(25.5)
+    path = tmp_path / "rec.npz"
+    save_record(path, rec)
+    back = load_record(path)
+    assert np.array_equal(back.timings, rec.timings) and back.down_proj_block_size == 16
+    text = format_report(back)
+    assert "RmsRouterUpgate" in text and "streamed" in text
