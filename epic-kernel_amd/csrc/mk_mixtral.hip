@@ -127,6 +127,17 @@ struct KParams {
     uint32_t timeout_ticks;
     int32_t *scratch;
     int32_t work_sharing;
+    // attention side and LM head (opcodes 1-4, 7); attn == 0 when absent
+    int32_t attn;
+    const uint16_t *qkv, *attn_ln, *oproj, *lm_norm, *lm_head;
+    uint16_t *kc, *vc, *q_rope, *attn_out, *logits;
+    const float *rope_cos, *rope_sin;
+    float *lse_int, *out_int;
+    int32_t Hq, Hkv, D, V, T, P;
+    int32_t qkv_bs, kv_bs, lm_bs, lm_red;
+    uint32_t pos;
+    float attn_scale;
+    int32_t skip_red;
 };
 
 // Per-workgroup state that outlives a single instruction.
@@ -1038,6 +1049,448 @@ __device__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const 
 }
 
 // ---------------------------------------------------------------------------
+// attention side and LM head: opcodes 1-4 and 7 (python_vm.py:61-222, 321-345)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ bool need_attention(const KParams &p, const Ctx &c, int op, int layer) {
+    if (p.attn) return true;
+    report_error(p, MK_ERR_UNSUPPORTED_OPCODE, c, op, layer, 0, op);
+    return false;
+}
+
+// Wait until the counter each of the first n (<= 64) lanes of wave 0 points
+// at reaches `expected`.  Every control value is wave-uniform (ballot,
+// readfirstlane); the result is broadcast to the workgroup like wait_ge's.
+__device__ bool wait_lanes_ge(const KParams &p, SharedState &sh, const int32_t *mine, int n, int expected,
+                              const Ctx &c, int opcode, int layer) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        int ok = 1, nap = 1;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+            int v = expected;
+            if (lane < n) v = (int)ld_dev32(mine);
+            const uint64_t shortfall = __ballot(v < expected);
+            if (shortfall == 0) break;
+            const int other = __builtin_amdgcn_readfirstlane(
+                (int)__hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            if (other != 0) {
+                ok = 0;
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)p.timeout_ticks) {
+                if (lane == (int)__builtin_ctzll(shortfall)) report_error_lane(p, MK_ERR_TIMEOUT, c, opcode, layer, expected, v);
+                ok = 0;
+                break;
+            }
+            for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
+            if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
+        }
+        if (lane == 0) sh.flag = ok;
+    }
+    __syncthreads();
+    const bool ok = sh.flag != 0;
+    __syncthreads();
+    return ok;
+}
+
+// act[0 .. H/8) = bf16(w * bf16(h * 1/sqrt(mean(h^2) + eps))) of the current
+// hidden state (python_vm rms_norm, lat/python_vm.py:50-56).  Ends with a
+// workgroup barrier.
+__device__ void rms_to_lds(const KParams &p, SharedState &sh, u32x4 *act, const uint16_t *w) {
+    const int tid = threadIdx.x, nv = p.H >> 3;
+    float ss = 0.f;
+    for (int v = tid; v < nv; v += kThreads) ss += sumsq8(ld_dev128(p.hidden, (uint32_t)v * 16u));
+    ss = block_sum(ss, sh.red_ss);
+    const float r = 1.0f / sqrtf(ss / (float)p.H + p.eps);
+    const u32x4 *w4 = reinterpret_cast<const u32x4 *>(w);
+    for (int v = tid; v < nv; v += kThreads) act[v] = norm8(ld_dev128(p.hidden, (uint32_t)v * 16u), w4[v], r);
+    __syncthreads();
+}
+
+// Rows [r0, r0 + nrows) (nrows even) of a row-major bf16 matrix with row
+// stride `ld` (elements), columns [col0, col0 + nc * 512), dotted with the
+// LDS vector x (8 bf16 per u32x4, starting at column col0); pairs of rows per
+// wave item, claimed from the LDS counter (reset by the caller before a
+// barrier).  fn(row, fp32 sum) is called by lane 0 of the wave.
+template <typename Fn>
+__device__ __forceinline__ void matvec_rows(SharedState &sh, const uint16_t *mat, size_t ld, int col0, int nc,
+                                            const u32x4 *x, int r0, int nrows, Fn fn) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
+        const int ra = r0 + 2 * it;
+        float aa = 0.f, ab = 0.f;
+        dot_pair(mat + (size_t)ra * ld + col0, mat + (size_t)(ra + 1) * ld + col0, x, x, nc, lane, aa, ab);
+        aa = wave_sum(aa);
+        ab = wave_sum(ab);
+        if (lane == 0) {
+            fn(ra, aa);
+            fn(ra + 1, ab);
+        }
+    }
+}
+
+// ---- opcode 1: Mixtral_QKV  (python_vm.py:61-118) -------------------------
+
+__device__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+                       int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
+    if (!need_attention(p, c, 1, layer)) return false;
+    const int D = p.D, qkv_rows = (p.Hq + 2 * p.Hkv) * D;
+    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.qkv_bs > qkv_rows) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 1, layer, b0, b1);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 1, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    rms_to_lds(p, sh, act, p.attn_ln + (size_t)layer * p.H);
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+
+    const int r0 = b0 * p.qkv_bs, nrows = (b1 - b0) * p.qkv_bs;
+    float *rowv = reinterpret_cast<float *>(act + (p.H >> 3));  // the block's outputs, bf16-rounded
+    matvec_rows(sh, p.qkv + (size_t)layer * qkv_rows * p.H, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
+                [&](int r, float s) { rowv[r - r0] = rbf(s); });
+    __syncthreads();
+
+    // RoPE on q and k rows (interleaved pairs (2i, 2i+1) share cos/sin[2i]):
+    // y = x * cos + rot(x) * sin in fp32 without contraction, rot(a, b) =
+    // (-b, a); then q -> q_post_rope, k/v -> the caches at pos_id.
+    const int k0 = p.Hq * D, v0 = k0 + p.Hkv * D;
+    const size_t kv_base = ((size_t)layer * p.T + p.pos) * (size_t)(p.Hkv * D);
+    for (int i = threadIdx.x; i < nrows; i += kThreads) {
+        const int r = r0 + i;
+        float y = rowv[i];
+        if (r < v0) {
+            const int d = r % D;
+            const float partner = rowv[i ^ 1];
+            const float cs = p.rope_cos[(size_t)p.pos * D + d], sn = p.rope_sin[(size_t)p.pos * D + d];
+            y = __fadd_rn(__fmul_rn(y, cs), __fmul_rn((d & 1) ? partner : -partner, sn));
+        }
+        const uint32_t bits = f2bf(y);
+        if (r < k0)
+            st_dev16(p.q_rope + r, bits);
+        else if (r < v0)
+            st_dev16(p.kc + kv_base + (r - k0), bits);
+        else
+            st_dev16(p.vc + kv_base + (r - v0), bits);
+    }
+    drain_and_sync();
+    // one arrival per block on its head's counter
+    const int bph = D / p.qkv_bs;
+    for (int b = b0 + (int)threadIdx.x; b < b1; b += kThreads)
+        __hip_atomic_fetch_add(bar_at(p, layer, 1) + b / bph, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// ---- opcode 2: Mixtral_PartialAttn  (python_vm.py:125-159) ----------------
+
+// Sum over each group of G consecutive lanes (G = 8 or 16); every lane of a
+// group ends with the group's sum.
+__device__ __forceinline__ float group_sum(float v, int G) {
+    v += dpp_add_src<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_add_src<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_add_src<0x141>(v);  // row_half_mirror: groups of 8
+    if (G == 16) v += dpp_add_src<0x140>(v);  // row_mirror: groups of 16
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int GQA>
+__device__ bool partial_attn(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c, int layer, int kv,
+                             int nparts, int pidx, int32_t *tim) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int D = p.D, G = D / 8, TPW = 64 / G;
+    const int slot = lane / G, dp = lane % G;
+    const int h0 = kv * GQA;
+
+    // producers: the GQA query heads, the key head and the value head
+    const int bph = D / p.qkv_bs;
+    const int32_t *bar_qkv = bar_at(p, layer, 1);
+    const int32_t *mine = bar_qkv + (lane < GQA ? h0 + lane : lane == GQA ? p.Hq + kv : p.Hq + p.Hkv + kv);
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_lanes_ge(p, sh, mine, GQA + 2, bph, c, 2, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+
+    const int seq = (int)p.pos + 1;
+    const int total = (seq + p.kv_bs - 1) / p.kv_bs;
+    const int per = (total + nparts - 1) / nparts;
+    const int tb0 = pidx * per, tb1 = min(tb0 + per, total);
+    const int t0 = tb0 * p.kv_bs, t1 = min(tb1 * p.kv_bs, seq);
+
+    float q[GQA][8];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) {
+        const u32x4 qv = ld_dev128(p.q_rope, (uint32_t)(((h0 + h) * D + dp * 8) * 2));
+        const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            q[h][2 * j] = bf2f(w[j] & 0xffffu);
+            q[h][2 * j + 1] = bf2f(w[j] >> 16);
+        }
+    }
+    float m[GQA], l[GQA], acc[GQA][8];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
+    }
+    // K and V of this layer and KV head: position t at byte (t * Hkv * D) * 2
+    const uint16_t *kbase = p.kc + (size_t)layer * p.T * p.Hkv * D + (size_t)kv * D;
+    const uint16_t *vbase = p.vc + (size_t)layer * p.T * p.Hkv * D + (size_t)kv * D;
+    const uint32_t row_bytes = (uint32_t)(p.Hkv * D * 2);
+    const int steps = (t1 - t0 + TPW - 1) / TPW;  // <= 0 for an empty partition
+    for (int st = wave; st < steps; st += kWaves) {
+        const int t = t0 + st * TPW + slot;
+        const bool valid = t < t1;
+        const uint32_t off = (uint32_t)(valid ? t : t0) * row_bytes + (uint32_t)dp * 16u;
+        const u32x4 kx = ld_dev128(kbase, off);
+        const u32x4 vx = ld_dev128(vbase, off);
+        const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
+        const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s = fmaf(q[h][2 * j], bf2f(kw[j] & 0xffffu), s);
+                s = fmaf(q[h][2 * j + 1], bf2f(kw[j] >> 16), s);
+            }
+            s = group_sum(s, G) * p.attn_scale;
+            if (!valid) s = -INFINITY;
+            const float mn = fmaxf(m[h], wave_max(s));  // finite: the step has a valid token
+            const float alpha = expf(m[h] - mn);        // 0 while m is -inf
+            const float pr = valid ? expf(s - mn) : 0.f;
+            l[h] = l[h] * alpha + (dp == 0 ? pr : 0.f);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[h][2 * j] = acc[h][2 * j] * alpha + pr * bf2f(vw[j] & 0xffffu);
+                acc[h][2 * j + 1] = acc[h][2 * j + 1] * alpha + pr * bf2f(vw[j] >> 16);
+            }
+            m[h] = mn;
+        }
+    }
+    // fold the token slots of the wave together (lanes with the same dp);
+    // l is carried by the dp == 0 lane of each slot, so a wave sum totals it
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) {
+        for (int o = G; o < 64; o <<= 1) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] += __shfl_xor(acc[h][j], o);
+        }
+        l[h] = wave_sum(l[h]);
+    }
+    // per-wave partials to LDS: m, l [kWaves][GQA], acc [kWaves][GQA][D]
+    float *wm = reinterpret_cast<float *>(act);
+    float *wl = wm + kWaves * GQA;
+    float *wacc = wl + kWaves * GQA;
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+            wm[wave * GQA + h] = m[h];
+            wl[wave * GQA + h] = l[h];
+        }
+    }
+    if (slot == 0) {
+#pragma unroll
+        for (int h = 0; h < GQA; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wacc[(wave * GQA + h) * D + dp * 8 + j] = acc[h][j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < GQA * D; i += kThreads) {
+        const int h = i / D, d = i % D;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w * GQA + h]);
+        float L = 0.f, O = 0.f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < kWaves; ++w) {
+                const float mw = wm[w * GQA + h];
+                if (mw == -INFINITY) continue;
+                const float f = expf(mw - M);
+                L += wl[w * GQA + h] * f;
+                O += wacc[(w * GQA + h) * D + d] * f;
+            }
+        }
+        const float out = L > 0.f ? O / L : 0.f;
+        if (p.skip_red) {
+            st_dev16(p.attn_out + (h0 + h) * D + d, f2bf(out));
+        } else {
+            st_dev32(p.out_int + ((size_t)(h0 + h) * p.P + pidx) * D + d, __float_as_uint(out));
+            if (d == 0) {
+                const float lse = L > 0.f ? log2f(L) + M * kLog2e : -INFINITY;
+                st_dev32(p.lse_int + (size_t)(h0 + h) * p.P + pidx, __float_as_uint(lse));
+            }
+        }
+    }
+    drain_and_sync();
+    if (p.skip_red)
+        arrive(bar_at(p, layer, 3), GQA);
+    else if (threadIdx.x < GQA)
+        __hip_atomic_fetch_add(bar_at(p, layer, 2) + h0 + threadIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+__device__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+                                int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int kv = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int nparts = __builtin_amdgcn_readfirstlane(ins[3]);
+    const int pidx = __builtin_amdgcn_readfirstlane(ins[4]);
+    if (!need_attention(p, c, 2, layer)) return false;
+    if (layer < 0 || layer >= p.num_layers || kv < 0 || kv >= p.Hkv || nparts < 1 || pidx < 0 || pidx >= nparts ||
+        (!p.skip_red && pidx >= p.P)) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 2, layer, kv, pidx);
+        return false;
+    }
+    switch (p.Hq / p.Hkv) {
+    case 1: return partial_attn<1>(p, sh, act, c, layer, kv, nparts, pidx, tim);
+    case 2: return partial_attn<2>(p, sh, act, c, layer, kv, nparts, pidx, tim);
+    default: return partial_attn<4>(p, sh, act, c, layer, kv, nparts, pidx, tim);
+    }
+}
+
+// ---- opcode 3: Mixtral_AttnReduction  (python_vm.py:166-189) --------------
+
+__device__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32_t *ins, const Ctx &c,
+                                  int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int hs = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int nparts = __builtin_amdgcn_readfirstlane(ins[3]);
+    const int terminal = __builtin_amdgcn_readfirstlane(ins[4]);
+    const int n = __builtin_amdgcn_readfirstlane(ins[5]);
+    if (!need_attention(p, c, 3, layer)) return false;
+    const int gqa = p.Hq / p.Hkv;
+    const int out_slot = (n >= 0 && n <= MK_INTS_PER_INSTRUCTION - 7) ? __builtin_amdgcn_readfirstlane(ins[6 + n]) : -1;
+    bool bad = layer < 0 || layer >= p.num_layers || hs < 0 || hs + gqa > p.Hq || n < 1 ||
+               n > MK_INTS_PER_INSTRUCTION - 7 || (!terminal && (out_slot < 0 || out_slot >= p.P));
+    for (int i = 0; !bad && i < n; ++i) {
+        const int s = ins[6 + i];
+        bad = s < 0 || s >= p.P;
+    }
+    if (bad) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 3, layer, hs, n);
+        return false;
+    }
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, layer, 2) + hs, nparts, c, 3, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    const int D = p.D;
+    for (int i = threadIdx.x; i < gqa * D; i += kThreads) {
+        const int h = hs + i / D, d = i % D;
+        float M = -INFINITY;
+        for (int k = 0; k < n; ++k) M = fmaxf(M, __uint_as_float(ld_dev32(p.lse_int + (size_t)h * p.P + ins[6 + k])));
+        float den = 0.f, num = 0.f;
+        for (int k = 0; k < n; ++k) {
+            const int s = ins[6 + k];
+            const float f = exp2f(__uint_as_float(ld_dev32(p.lse_int + (size_t)h * p.P + s)) - M);
+            den += f;
+            num += __uint_as_float(ld_dev32(p.out_int + ((size_t)h * p.P + s) * D + d)) * f;
+        }
+        const float red = num / den;
+        if (terminal) {
+            st_dev16(p.attn_out + h * D + d, f2bf(red));
+        } else {
+            st_dev32(p.out_int + ((size_t)h * p.P + out_slot) * D + d, __float_as_uint(red));
+            if (d == 0) st_dev32(p.lse_int + (size_t)h * p.P + out_slot, __float_as_uint(logf(den)));
+        }
+    }
+    drain_and_sync();
+    arrive(bar_at(p, layer, 3), gqa);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// ---- opcode 4: Mixtral_OProj  (python_vm.py:196-215) ----------------------
+
+__device__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+                         int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
+    const int red = __builtin_amdgcn_readfirstlane(ins[4]);
+    if (!need_attention(p, c, 4, layer)) return false;
+    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.oproj_bs > p.H || red != 0) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 4, layer, b0, b1);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, layer, 3), p.Hq, c, 4, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    const int K = p.Hq * p.D;  // reduction length
+    for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(p.attn_out, (uint32_t)v * 16u);
+    __syncthreads();
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    matvec_rows(sh, p.oproj + (size_t)layer * p.H * K, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs,
+                (b1 - b0) * p.oproj_bs, [&](int r, float s) {
+                    uint16_t *hp = p.hidden + r;
+                    st_dev16(hp, f2bf(bf2f(ld_dev16(hp)) + rbf(s)));
+                });
+    drain_and_sync();
+    arrive(bar_at(p, layer, 4), b1 - b0);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// ---- opcode 7: Mixtral_RMS_LM_Head  (python_vm.py:321-345) ----------------
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+                           int32_t *tim) {
+    const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int red = __builtin_amdgcn_readfirstlane(ins[3]);
+    const int last = p.num_layers - 1;
+    if (!need_attention(p, c, 7, last)) return false;
+    if (b0 < 0 || b1 < b0 || (int64_t)b1 * p.lm_bs > p.V || red < 0 || (int64_t)(red + 1) * p.lm_red > p.H) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 7, last, b0, b1);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, last, 6), 2 * (p.H / p.down_bs), c, 7, last)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    rms_to_lds(p, sh, act, p.lm_norm);
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    // logits[r] += bf16(W[r, cols] . normed[cols]) for a pair of rows at a
+    // time: one packed bf16 atomic add per pair (rows are even-aligned)
+    const int col0 = red * p.lm_red;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = b0 * p.lm_bs, nrows = (b1 - b0) * p.lm_bs;
+    for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
+        const int ra = r0 + 2 * it;
+        float aa = 0.f, ab = 0.f;
+        dot_pair(p.lm_head + (size_t)ra * p.H + col0, p.lm_head + (size_t)(ra + 1) * p.H + col0, act + (col0 >> 3),
+                 act + (col0 >> 3), p.lm_red / kChunkElems, lane, aa, ab);
+        aa = wave_sum(aa);
+        ab = wave_sum(ab);
+        if (lane == 0) {
+            const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(aa)), __builtin_bit_cast(__bf16, (uint16_t)f2bf(ab))};
+            __builtin_amdgcn_global_atomic_fadd_v2bf16(
+                (__attribute__((address_space(1))) bf16x2_t *)(p.logits + ra), v);
+        }
+    }
+    drain_and_sync();
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// ---------------------------------------------------------------------------
 // the persistent interpreter
 // ---------------------------------------------------------------------------
 
@@ -1059,17 +1512,14 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         bool ok = true;
         switch (op) {
         case 0: break;
+        case 1: ok = op_qkv(p, sh, act, ins, c, tim); break;
+        case 2: ok = op_partial_attn(p, sh, act, ins, c, tim); break;
+        case 3: ok = op_attn_reduction(p, sh, ins, c, tim); break;
+        case 4: ok = op_oproj(p, sh, act, ins, c, tim); break;
         case 5: ok = op_rms_router_upgate<kE>(p, sh, act, ins, c, tim); break;
         case 6: ok = op_expert_downproj(p, sh, act, ins, c, tim); break;
+        case 7: ok = op_lm_head(p, sh, act, ins, c, tim); break;
         case 8: ok = op_predict<kE>(p, sh, act, ins, c, tim); break;
-        case 1:
-        case 2:
-        case 3:
-        case 4:
-        case 7:
-            report_error(p, MK_ERR_UNSUPPORTED_OPCODE, c, op, __builtin_amdgcn_readfirstlane(ins[1]), 0, op);
-            ok = false;
-            break;
         default:
             report_error(p, MK_ERR_BAD_OPCODE, c, op, 0, 0, op);
             ok = false;
@@ -1163,7 +1613,47 @@ size_t lds_bytes_for(const mk_mixtral_globals *g) {
     // both SiLU rows, then the opcode-6 cache-warming sink (1 KiB per wave)
     const size_t silu = (size_t)g->intermediate_size * 2 * 2 + (size_t)kWaves * 1024;
     size_t need = normed > silu ? normed : silu;
+    if (g->qkv_weights != nullptr) {
+        const size_t Hq = (size_t)g->num_attention_heads, Hkv = (size_t)g->num_kv_heads, D = (size_t)g->head_dim;
+        // opcode 1: normed hidden + one fp32 per QKV row; opcode 2: per-wave
+        // softmax partials; opcode 4: attn_out
+        const size_t qkv = normed + (Hq + 2 * Hkv) * D * 4;
+        const size_t attn = (size_t)kWaves * (Hq / Hkv) * (D + 2) * 4;
+        const size_t oproj = Hq * D * 2;
+        need = need > qkv ? need : qkv;
+        need = need > attn ? need : attn;
+        need = need > oproj ? need : oproj;
+    }
     return need > (size_t)kMinLdsBytes ? need : (size_t)kMinLdsBytes;
+}
+
+// The attention tensors are optional (an MoE-only launch passes none); when
+// qkv_weights is set, every attention field must be consistent.
+int validate_attention(const mk_mixtral_globals *g) {
+    if (g->qkv_weights == nullptr) return MK_OK;
+    if (!g->attn_norm_weights || !g->o_weights || !g->lm_head_norm_weights || !g->lm_head_weights || !g->k_cache ||
+        !g->v_cache || !g->rope_cos || !g->rope_sin || !g->q_post_rope || !g->attn_out ||
+        !g->attn_lse_intermediates || !g->attn_out_intermediates || !g->logits)
+        return MK_ERR_INVALID_ARGUMENT;
+    const int Hq = g->num_attention_heads, Hkv = g->num_kv_heads, D = g->head_dim;
+    if (Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 4 || (Hq / Hkv) & (Hq / Hkv - 1)) return MK_ERR_UNSUPPORTED;
+    if (D != 64 && D != 128) return MK_ERR_UNSUPPORTED;
+    if ((Hq * D) % kChunkElems) return MK_ERR_UNSUPPORTED;
+    if (g->qkv_block_size < 2 || g->qkv_block_size % 2 || D % g->qkv_block_size) return MK_ERR_INVALID_ARGUMENT;
+    if (g->o_proj_block_size % 2 || g->lm_head_block_size < 2 || g->lm_head_block_size % 2) return MK_ERR_INVALID_ARGUMENT;
+    if (g->attn_kv_block_size < 1 || g->vocab_size < 1 || g->vocab_size % g->lm_head_block_size)
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->lm_head_reduction < kChunkElems || g->lm_head_reduction % kChunkElems) return MK_ERR_INVALID_ARGUMENT;
+    if (g->kv_capacity < 1 || (int64_t)g->pos_id >= g->kv_capacity || g->attn_partial_slots < 1)
+        return MK_ERR_INVALID_ARGUMENT;
+    // KV slabs are addressed with 32-bit byte offsets per layer
+    if ((int64_t)g->kv_capacity * Hkv * D * 2 > (INT64_C(1) << 31) - 1) return MK_ERR_UNSUPPORTED;
+    if (!aligned16(g->qkv_weights) || !aligned16(g->o_weights) || !aligned16(g->lm_head_weights) ||
+        !aligned16(g->k_cache) || !aligned16(g->v_cache) || !aligned16(g->q_post_rope) || !aligned16(g->attn_out) ||
+        !aligned16(g->attn_norm_weights) || !aligned16(g->lm_head_norm_weights) ||
+        (reinterpret_cast<uintptr_t>(g->logits) & 3u))
+        return MK_ERR_INVALID_ARGUMENT;
+    return MK_OK;
 }
 
 int validate(const mk_mixtral_globals *g) {
@@ -1195,7 +1685,7 @@ int validate(const mk_mixtral_globals *g) {
                          g->predictor_weights};
     for (const void *v : vec)
         if (v != nullptr && !aligned16(v)) return MK_ERR_INVALID_ARGUMENT;
-    return MK_OK;
+    return validate_attention(g);
 }
 
 }  // namespace
@@ -1314,6 +1804,34 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.timeout_ticks = ticks > 0xffffffffu ? 0xffffffffu : (uint32_t)ticks;
     kp.scratch = st->scratch;
     kp.work_sharing = g->work_sharing ? 1 : 0;
+    kp.attn = g->qkv_weights != nullptr;
+    kp.qkv = g->qkv_weights;
+    kp.attn_ln = g->attn_norm_weights;
+    kp.oproj = g->o_weights;
+    kp.lm_norm = g->lm_head_norm_weights;
+    kp.lm_head = g->lm_head_weights;
+    kp.kc = g->k_cache;
+    kp.vc = g->v_cache;
+    kp.q_rope = g->q_post_rope;
+    kp.attn_out = g->attn_out;
+    kp.logits = g->logits;
+    kp.rope_cos = g->rope_cos;
+    kp.rope_sin = g->rope_sin;
+    kp.lse_int = g->attn_lse_intermediates;
+    kp.out_int = g->attn_out_intermediates;
+    kp.Hq = g->num_attention_heads;
+    kp.Hkv = g->num_kv_heads;
+    kp.D = g->head_dim;
+    kp.V = g->vocab_size;
+    kp.T = g->kv_capacity;
+    kp.P = g->attn_partial_slots;
+    kp.qkv_bs = g->qkv_block_size;
+    kp.kv_bs = g->attn_kv_block_size;
+    kp.lm_bs = g->lm_head_block_size;
+    kp.lm_red = g->lm_head_reduction;
+    kp.pos = g->pos_id;
+    kp.attn_scale = g->attn_scale;
+    kp.skip_red = g->skip_attn_reduction ? 1 : 0;
 
     if (e8)
         hipLaunchKernelGGL(mk_mixtral_kernel<8>, dim3((unsigned)g->num_workers), dim3(kThreads), lds,

@@ -41,6 +41,9 @@ def interpret_with_mk(globs: MixtralGlobals, mk_func, **launch_kwargs):
         expert_proj_block_size=globs.expert_proj_block_size,
         down_proj_block_size=globs.down_proj_block_size,
         o_proj_block_size=globs.o_proj_block_size,
+        qkv_block_size=globs.qkv_block_size,
+        attn_kv_block_size=globs.attn_kv_block_size,
+        lm_head_block_size=globs.lm_head_block_size,
         router_bias=globs.router_bias,
         predictor_weights=None if globs.predictor_weights is None else _flatten_depth(globs.predictor_weights),
         stream=(torch.cuda.current_stream(globs.hidden_states.device)

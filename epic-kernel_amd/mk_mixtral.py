@@ -54,7 +54,7 @@ __all__ = [
 _HERE = Path(__file__).resolve().parent
 _LIB_NAME = "libmk_mixtral.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 STATUS_WORDS = 16
 MAX_EXPERTS = 16
 
@@ -142,6 +142,16 @@ class MkMixtralGlobals(ctypes.Structure):
         ("expert_proj_block_size", ctypes.c_int32),
         ("down_proj_block_size", ctypes.c_int32),
         ("o_proj_block_size", ctypes.c_int32),
+        ("qkv_block_size", ctypes.c_int32),
+        ("attn_kv_block_size", ctypes.c_int32),
+        ("lm_head_block_size", ctypes.c_int32),
+        ("lm_head_reduction", ctypes.c_int32),
+        ("num_attention_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("vocab_size", ctypes.c_int32),
+        ("kv_capacity", ctypes.c_int32),
+        ("attn_partial_slots", ctypes.c_int32),
         ("router_bias", _P),
         ("predictor_weights", _P),
         ("status", _P),
@@ -288,6 +298,10 @@ def build_globals_struct(
     expert_proj_block_size: int = 16,
     down_proj_block_size: int = 16,
     o_proj_block_size: int = 16,
+    qkv_block_size: int = 16,
+    attn_kv_block_size: int = 16,
+    lm_head_block_size: int = 16,
+    lm_head_reduction: int = 2048,
     router_bias=None,
     predictor_weights=None,
     status=None,
@@ -350,6 +364,11 @@ def build_globals_struct(
     if status is not None:
         _check_tensor("status", status, torch.int32, dev, min_numel=STATUS_WORDS)
 
+    attn = _attention_shape(qkv_weights, attn_norm_weights, o_weights, lm_head_norm_weights, lm_head_weights,
+                            k_cache, v_cache, rope_cos, rope_sin, q_post_rope, attn_out, attn_lse_intermediates,
+                            attn_out_intermediates, logits, L, H, int(pos_id), dev, int(qkv_block_size),
+                            int(attn_kv_block_size), int(lm_head_block_size), int(lm_head_reduction))
+
     g = MkMixtralGlobals()
     g.struct_size = ctypes.sizeof(MkMixtralGlobals)
     g.abi_version = ABI_VERSION
@@ -385,6 +404,15 @@ def build_globals_struct(
     g.expert_proj_block_size = int(expert_proj_block_size)
     g.down_proj_block_size = int(down_proj_block_size)
     g.o_proj_block_size = int(o_proj_block_size)
+    if attn is not None:
+        (g.qkv_block_size, g.attn_kv_block_size, g.lm_head_block_size, g.lm_head_reduction,
+         g.num_attention_heads, g.num_kv_heads, g.head_dim, g.vocab_size, g.kv_capacity,
+         g.attn_partial_slots) = attn
+    else:
+        for name in ("qkv_weights", "attn_norm_weights", "o_weights", "lm_head_norm_weights", "lm_head_weights",
+                     "k_cache", "v_cache", "rope_cos", "rope_sin", "q_post_rope", "attn_out",
+                     "attn_lse_intermediates", "attn_out_intermediates", "logits"):
+            setattr(g, name, None)
     g.router_bias = None if router_bias is None else router_bias.data_ptr()
     g.predictor_weights = None if predictor_weights is None else predictor_weights.data_ptr()
     g.status = None if status is None else status.data_ptr()
@@ -392,6 +420,47 @@ def build_globals_struct(
     g.record_timings = int(bool(record_timings))
     g.work_sharing = int(bool(work_sharing))
     return g
+
+
+def _attention_shape(qkv, attn_ln, o_proj, lm_norm, lm_head, k_cache, v_cache, rope_cos, rope_sin, q_rope,
+                     attn_out, lse_int, out_int, logits, L, H, pos_id, dev, qkv_bs, kv_bs, lm_bs, lm_red):
+    """Validate the attention-side tensors; None when they are absent (the
+    MoE-only launch), else the struct's attention shape fields."""
+    if not (isinstance(qkv, torch.Tensor) and qkv.numel()):
+        return None
+    bf16 = torch.bfloat16
+    _check(k_cache.dim() == 4, "k_cache must be [L*B, T, Hkv, D] (batch 1)")
+    LB, T, Hkv, D = k_cache.shape
+    _check(LB == L, f"k_cache has {LB} layer rows, expected {L} (batch 1)")
+    _check(D in (64, 128), f"head_dim must be 64 or 128, got {D}")
+    _check_tensor("attn_lse_intermediates", lse_int, torch.float32, dev)
+    _check(lse_int.dim() == 2, "attn_lse_intermediates must be [Hq, P]")
+    Hq, P = lse_int.shape
+    _check(Hkv > 0 and Hq % Hkv == 0 and Hq // Hkv in (1, 2, 4), f"need Hq / Hkv in (1, 2, 4), got {Hq} / {Hkv}")
+    QKV = (Hq + 2 * Hkv) * D
+    _check_tensor("qkv_weights", qkv, bf16, dev, (L, QKV, H))
+    _check_tensor("attn_norm_weights", attn_ln, bf16, dev, (L, H))
+    _check_tensor("o_weights", o_proj, bf16, dev, (L, H, Hq * D))
+    _check_tensor("k_cache", k_cache, bf16, dev, (L, T, Hkv, D))
+    _check_tensor("v_cache", v_cache, bf16, dev, (L, T, Hkv, D))
+    _check_tensor("rope_cos", rope_cos, torch.float32, dev, min_numel=T * D)
+    _check(rope_cos.dim() == 2 and rope_cos.shape[1] == D and rope_cos.shape[0] >= T, "rope_cos must be [T, D]")
+    _check_tensor("rope_sin", rope_sin, torch.float32, dev, tuple(rope_cos.shape))
+    _check_tensor("q_post_rope", q_rope, bf16, dev, (Hq * D,))
+    _check_tensor("attn_out", attn_out, bf16, dev, (Hq * D,))
+    _check_tensor("attn_out_intermediates", out_int, torch.float32, dev, (Hq, P, D))
+    _check_tensor("logits", logits, bf16, dev)
+    V = logits.numel()
+    _check(logits.dim() == 1, "logits must be [V]")
+    _check_tensor("lm_head_norm_weights", lm_norm, bf16, dev, min_numel=H)
+    _check(lm_norm.numel() == H, "lm_head_norm_weights must have H elements")
+    _check_tensor("lm_head_weights", lm_head, bf16, dev, (V, H))
+    _check(0 <= pos_id < T, f"pos_id {pos_id} outside the KV cache ({T} positions)")
+    _check(qkv_bs > 0 and D % qkv_bs == 0 and qkv_bs % 2 == 0, f"qkv_block_size {qkv_bs} must be even and divide {D}")
+    _check(kv_bs > 0, "attn_kv_block_size must be positive")
+    _check(lm_bs > 0 and lm_bs % 2 == 0 and V % lm_bs == 0, f"lm_head_block_size {lm_bs} must be even, divide {V}")
+    _check(lm_red % 512 == 0 and lm_red > 0, "lm_head_reduction must be a multiple of 512")
+    return qkv_bs, kv_bs, lm_bs, lm_red, Hq, Hkv, D, V, T, P
 
 
 def launch_struct(g: MkMixtralGlobals, device: torch.device, stream=None) -> None:

@@ -21,22 +21,32 @@
  *
  * Instruction queues: `instructions[num_workers][queue_len][32]` int32, the
  * serialised layout of megakernels/instructions.py:97-119.  Worker w (one
- * workgroup, one compute unit) runs queue w in order.  Implemented opcodes:
+ * workgroup, one compute unit) runs queue w in order.  Opcodes:
  *   0 NoOp
+ *   1 Mixtral_QKV               [1, layer, start_block, end_block]
+ *   2 Mixtral_PartialAttn       [2, layer, kv_head, num_partials, partial_idx]
+ *   3 Mixtral_AttnReduction     [3, layer, head_start, num_partials, is_terminal,
+ *                                n, list[n]..., output_partial_idx]
+ *   4 Mixtral_OProj             [4, layer, start_block, end_block, reduction_block=0]
  *   5 RmsRouterUpgate           [5, layer, start_block, num_blocks]
  *   6 ExpertDownProjFused       [6, layer, start_block, end_block, reduction_block=0]
+ *   7 Mixtral_RMS_LM_Head       [7, start_block, end_block, reduction_block]
  *   8 SpeculativeExpertPredict  [8, layer]
- * Opcodes 1-4 and 7 (attention, LM head) are rejected with
- * MK_ERR_UNSUPPORTED_OPCODE.
+ * Opcodes 1-4 and 7 need the attention tensors (qkv_weights non-NULL);
+ * without them they are rejected with MK_ERR_UNSUPPORTED_OPCODE.
  *
  * Barriers: `barriers[bar_layers][bar_ops][bar_width]` int32, counter for
- * (layer, opcode) at [layer][opcode-1][0].  Waits proceed once a counter is
+ * (layer, opcode) at [layer][opcode-1][idx].  Waits proceed once a counter is
  * >= the expected arrival count (so pre-filled barriers satisfy them):
+ *   opcode 1 waits [l-1][5][0] >= k * hidden / down_proj_block_size (l > 0)
+ *   opcode 2 waits [l][0][h] >= head_dim / qkv_block_size for its heads
+ *   opcode 3 waits [l][1][head_start] >= num_partials
+ *   opcode 4 waits [l][2][0] >= num_attention_heads
  *   opcode 5 waits [l][3][0] >= hidden / o_proj_block_size
  *   opcode 6 waits [l][4][0] >= intermediate / expert_proj_block_size
+ *   opcode 7 waits [L-1][5][0] >= k * hidden / down_proj_block_size
  *   opcode 8 waits [l-1][5][0] >= k * hidden / down_proj_block_size (l > 0)
- * and arrive with +num_blocks, +k*(end-start), +1 respectively
- * (megakernels/mixtral/python_vm.py:38-54,228-371).
+ * and arrive as megakernels/mixtral/python_vm.py:38-371 does.
  *
  * Device-side failures (barrier spin time-out, bad opcode or operand) are
  * recorded in a status word and make every worker exit; they are read back
@@ -51,7 +61,7 @@
 extern "C" {
 #endif
 
-#define MK_MIXTRAL_ABI_VERSION 1
+#define MK_MIXTRAL_ABI_VERSION 2
 #define MK_INTS_PER_INSTRUCTION 32
 #define MK_TIMING_SLOTS 128
 #define MK_STATUS_WORDS 16
@@ -107,10 +117,10 @@ typedef struct mk_mixtral_globals {
     int64_t num_workers, queue_len;
     int32_t *timings;              /* [num_workers, queue_len, 128] or NULL */
 
-    /* attention weights (mixtral.cuh:160-162): accepted, unused by 0/5/6/8 */
-    const void *qkv_weights;
-    const void *attn_norm_weights;
-    const void *o_weights;
+    /* attention weights (mixtral.cuh:160-162), bf16, NULL if absent */
+    const uint16_t *qkv_weights;        /* [L, (Hq + 2 Hkv) D, H] */
+    const uint16_t *attn_norm_weights;  /* [L, H]                 */
+    const uint16_t *o_weights;          /* [L, H, Hq D]           */
 
     /* MoE weights (mixtral.cuh:165-169), bf16, row-major */
     const uint16_t *expert_gate_weights;  /* [L*E, F, H] */
@@ -119,23 +129,23 @@ typedef struct mk_mixtral_globals {
     const uint16_t *router_weights;       /* [L*E, H]    */
     const uint16_t *ffn_ln_weights;       /* [L, H]      */
 
-    /* LM head, KV cache, RoPE (mixtral.cuh:172-181): accepted, unused */
-    const void *lm_head_norm_weights;
-    const void *lm_head_weights;
-    const void *k_cache;
-    const void *v_cache;
-    const float *rope_cos;
-    const float *rope_sin;
+    /* LM head, KV cache, RoPE (mixtral.cuh:172-181) */
+    const uint16_t *lm_head_norm_weights;  /* [H] bf16                     */
+    const uint16_t *lm_head_weights;       /* [V, H] bf16                  */
+    uint16_t *k_cache;                     /* [L, T, Hkv, D] bf16          */
+    uint16_t *v_cache;                     /* [L, T, Hkv, D] bf16          */
+    const float *rope_cos;                 /* [T, D] fp32, interleaved     */
+    const float *rope_sin;                 /* [T, D] fp32                  */
 
     /* activations (mixtral.cuh:184-191) */
-    uint16_t *hidden_states;       /* [H] bf16, updated in place by opcode 6 */
-    void *q_post_rope;
-    void *attn_out;
-    float *attn_lse_intermediates;
-    float *attn_out_intermediates;
+    uint16_t *hidden_states;       /* [H] bf16, updated in place by opcodes 4 and 6 */
+    uint16_t *q_post_rope;         /* [Hq D] bf16                 */
+    uint16_t *attn_out;            /* [Hq D] bf16                 */
+    float *attn_lse_intermediates; /* [Hq, P] fp32                */
+    float *attn_out_intermediates; /* [Hq, P, D] fp32             */
     uint16_t *expert_silu_out;     /* [E, F] bf16 */
     uint16_t *router_normed_hidden;/* [H] bf16 */
-    void *logits;
+    uint16_t *logits;              /* [V] bf16, accumulated by opcode 7 (caller zeroes) */
 
     /* router outputs (mixtral.cuh:194-198) */
     int32_t *selected_expert_indices;   /* [k] */
@@ -159,6 +169,20 @@ typedef struct mk_mixtral_globals {
     int32_t expert_proj_block_size;
     int32_t down_proj_block_size;
     int32_t o_proj_block_size;
+
+    /* attention and LM-head shape (compiled into the reference kernel,
+     * demos/mixtral/mixtral.cuh:22-35; MixtralGlobals block sizes).  Only read
+     * by opcodes 1-4 and 7; all zero when the attention tensors are absent. */
+    int32_t qkv_block_size;        /* rows per QKV block (16)                */
+    int32_t attn_kv_block_size;    /* KV positions per attention block (16)  */
+    int32_t lm_head_block_size;    /* logit rows per LM-head block (16)      */
+    int32_t lm_head_reduction;     /* columns per LM-head reduction block (2048) */
+    int32_t num_attention_heads;   /* Hq                                     */
+    int32_t num_kv_heads;          /* Hkv; Hq / Hkv in {1, 2, 4}             */
+    int32_t head_dim;              /* D: 64 or 128                           */
+    int32_t vocab_size;            /* V                                      */
+    int32_t kv_capacity;           /* T: positions per layer in the KV cache */
+    int32_t attn_partial_slots;    /* P: columns of attn_*_intermediates     */
 
     /* extensions, no counterpart in the reference; NULL keeps its semantics */
     const float *router_bias;          /* [L*E] fp32 added to router logits  */

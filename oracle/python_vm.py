@@ -4,18 +4,23 @@ TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
 and the ``cpu_baseline`` leg of ``bench.py`` as the checker.  The product
 path (``epic-kernel_amd``) never imports it.
 
-A restatement of the reference's Python VM solvers for opcodes 5, 6 and 8:
+A restatement of the reference's Python VM solvers:
 
+* ``solve_qkv``                        megakernels/mixtral/python_vm.py:61-118
+* ``solve_partial_attn``               megakernels/mixtral/python_vm.py:125-159
+* ``solve_attn_reduction``             megakernels/mixtral/python_vm.py:166-189
+* ``solve_oproj``                      megakernels/mixtral/python_vm.py:196-215
 * ``solve_rms_router_upgate``          megakernels/mixtral/python_vm.py:228-277
 * ``solve_expert_downproj_fused``      megakernels/mixtral/python_vm.py:284-314
+* ``solve_lm_head``                    megakernels/mixtral/python_vm.py:321-345
 * ``solve_speculative_expert_predict`` megakernels/mixtral/python_vm.py:356-371
 * ``rms_norm`` / matvec helpers        megakernels/demos/latency/python_vm.py:23-56
 
 including the barrier assertions each solver makes before it runs and the
 increment it makes after.  The arithmetic of the bf16 matvecs and the RMS
 norm is in ``moe_oracle.c`` (same rounding points as torch's bf16 CPU ops);
-softmax, top-k and the score renormalisation use torch's fp32 CPU routines,
-exactly the calls the reference makes.
+softmax, top-k, the score renormalisation, RoPE and attention use torch's
+fp32 CPU routines, exactly the calls the reference makes.
 
 Pinning (what keeps this restatement honest, see ``tests/test_oracle.py``):
 rounding helpers against torch's own bf16 conversion; ``rms_norm`` against a
@@ -42,8 +47,15 @@ _PKG = _REPO / "epic-kernel_amd"
 if str(_PKG) not in sys.path:
     sys.path.insert(0, str(_PKG))
 
+import math  # noqa: E402
+
 from megakernels_amd.mixtral.instructions import (  # noqa: E402
     ExpertDownProjFused,
+    Mixtral_AttnReduction,
+    Mixtral_OProj,
+    Mixtral_PartialAttn,
+    Mixtral_QKV,
+    Mixtral_RMS_LM_Head,
     MixtralGlobals,
     RmsRouterUpgate,
     SpeculativeExpertPredict,
@@ -244,9 +256,162 @@ def solve_speculative_expert_predict(globs: MixtralGlobals, ins: SpeculativeExpe
     globs.barriers[layer, ins.opcode() - 1, 0] += 1
 
 
+# ---------------------------------------------------------------------------
+# attention side and LM head (mkm/python_vm.py:61-222, 321-345)
+# ---------------------------------------------------------------------------
+
+def rope_interleaved(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Interleaved RoPE of bf16 ``x`` with fp32 ``cos``/``sin`` of the same
+    length, returned in fp32: ``x * cos + rot(x) * sin`` with ``rot`` mapping
+    the pair (a, b) at (2i, 2i+1) to (-b, a) (``megakernels/llama.py:136-174``;
+    bf16 times fp32 promotes to fp32, as in the reference)."""
+    rot = torch.stack((-x[1::2], x[0::2]), dim=-1).reshape(x.shape)
+    return x * cos + rot * sin
+
+
+def solve_qkv(globs: MixtralGlobals, ins: Mixtral_QKV):
+    """mkm/python_vm.py:61-118."""
+    layer = ins.layer_idx
+    if layer > 0:
+        bar = globs.barriers[layer - 1, ExpertDownProjFused.opcode() - 1]
+        assert bar[0] == expected_downproj_barrier(globs), f"QKV layer {layer}: downproj barrier {int(bar[0])}"
+    post_ln = rms_norm(globs.hidden_states, globs.attn_ln_weights[layer], globs.rms_norm_eps)
+    pos = globs.pos_id
+    D = globs.head_dim
+    k_start = globs.num_attention_heads * D
+    v_start = k_start + globs.num_kv_heads * D
+    bs = globs.qkv_block_size
+    bph = D // bs
+    bars = globs.barriers[layer, ins.opcode() - 1]
+    for b in range(ins.start_output_block_idx, ins.end_output_block_idx):
+        start, end = b * bs, (b + 1) * bs
+        out = matvec(globs.qkv_proj_weights[layer], post_ln, start, bs)
+        if start < v_start:
+            seg = start % D
+            out = rope_interleaved(out, globs.rope_cos[pos, seg:seg + bs], globs.rope_sin[pos, seg:seg + bs])
+        if start < k_start:
+            globs.post_ln_rope_q[start:end] = out.to(torch.bfloat16)
+        elif start < v_start:
+            s0 = start - k_start
+            globs.k_cache[layer, :, pos].view(-1)[s0:s0 + bs] = out.to(torch.bfloat16)
+        else:
+            s0 = start - v_start
+            globs.v_cache[layer, :, pos].view(-1)[s0:s0 + bs] = out
+        bars[b // bph] += 1
+
+
+def attention_partial(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
+    """(lse [h], out [h, D]) of one split-KV partition in fp32, as
+    mkm/python_vm.py:145-149: ``lse = log2(sum(exp(q.k * scale)))``,
+    ``out = softmax(q.k * scale) @ v``; an empty partition gives lse = -inf
+    and out = 0."""
+    qk = (q.float() @ k.float().T) * scale
+    lse = torch.log2(torch.sum(torch.exp(qk), dim=-1))
+    if k.shape[0] == 0:
+        return lse, torch.zeros(q.shape[0], v.shape[-1], dtype=torch.float32)
+    return lse, torch.softmax(qk, dim=-1) @ v.float()
+
+
+def partial_token_range(seq_len: int, kv_block_size: int, num_partials: int, partial_idx: int):
+    """Tokens [start, end) of one partition (mkm/python_vm.py:133-140)."""
+    total = math.ceil(seq_len / kv_block_size)
+    per = math.ceil(total / num_partials)
+    b0 = partial_idx * per
+    b1 = min(b0 + per, total)
+    return b0 * kv_block_size, min(b1 * kv_block_size, seq_len)
+
+
+def solve_partial_attn(globs: MixtralGlobals, ins: Mixtral_PartialAttn):
+    """mkm/python_vm.py:125-159."""
+    gqa = globs.num_attention_heads // globs.num_kv_heads
+    bph = globs.head_dim // globs.qkv_block_size
+    layer, kv = ins.layer_idx, ins.kv_head_idx
+    bars = globs.barriers[layer, ins.prev_opcode() - 1]
+    for i in range(gqa):
+        assert bars[kv * gqa + i] == bph
+    assert bars[globs.num_attention_heads + kv] == bph
+    assert bars[globs.num_attention_heads + globs.num_kv_heads + kv] == bph
+    t0, t1 = partial_token_range(globs.pos_id + 1, globs.attn_kv_block_size, ins.num_partials, ins.partial_idx)
+    k = globs.k_cache[layer, 0, t0:t1, kv]
+    v = globs.v_cache[layer, 0, t0:t1, kv]
+    h0, h1 = kv * gqa, kv * gqa + gqa
+    q = globs.post_ln_rope_q.view(globs.num_attention_heads, -1)[h0:h1]
+    lse, out = attention_partial(q, k, v, globs.attn_scale)
+    if globs.skip_attn_reduction:
+        globs.attn_out.view(globs.num_attention_heads, -1)[h0:h1] = out.to(globs.attn_out.dtype)
+        globs.barriers[layer, Mixtral_AttnReduction.opcode() - 1, 0] += h1 - h0
+    else:
+        globs.attn_lse_intermediates[h0:h1, ins.partial_idx] = lse
+        globs.attn_out_intermediates[h0:h1, ins.partial_idx] = out
+        globs.barriers[layer, ins.opcode() - 1, h0:h1] += 1
+
+
+def combine_partials(lses: torch.Tensor, outs: torch.Tensor):
+    """(denominator [h, 1], reduced [h, D]) of partitions weighted by
+    ``2^(lse - max lse)`` (mkm/python_vm.py:176-179)."""
+    max_lse = torch.max(lses, dim=-1, keepdim=True).values
+    factors = (lses - max_lse).exp2()
+    denom = factors.sum(dim=-1, keepdim=True)
+    return denom, (outs * factors.unsqueeze(-1)).sum(dim=1) / denom
+
+
+def solve_attn_reduction(globs: MixtralGlobals, ins: Mixtral_AttnReduction):
+    """mkm/python_vm.py:166-189."""
+    h0 = ins.head_start_idx
+    n = globs.attn_reduction_size
+    assert globs.barriers[ins.layer_idx, ins.prev_opcode() - 1, h0] == ins.num_partials
+    idx = torch.tensor(ins.reduction_list, dtype=torch.long)
+    lses = globs.attn_lse_intermediates[h0:h0 + n, idx]
+    outs = globs.attn_out_intermediates[h0:h0 + n, idx]
+    denom, reduced = combine_partials(lses, outs)
+    if ins.is_terminal:
+        globs.attn_out.view(globs.num_attention_heads, -1)[h0:h0 + n] = reduced.to(globs.attn_out.dtype)
+    else:
+        slot = ins.output_partial_idx
+        globs.attn_lse_intermediates[h0:h0 + n, slot] = denom.log().squeeze(-1)
+        globs.attn_out_intermediates[h0:h0 + n, slot] = reduced
+    globs.barriers[ins.layer_idx, ins.opcode() - 1, 0] += n
+
+
+def solve_oproj(globs: MixtralGlobals, ins: Mixtral_OProj):
+    """mkm/python_vm.py:196-215 with lat/python_vm.py:59-80:
+    ``h[rows] = bf16(h[rows] + bf16(W[rows] @ attn_out))``."""
+    assert globs.barriers[ins.layer_idx, ins.prev_opcode() - 1, 0] == globs.num_attention_heads
+    assert ins.start_block_idx == ins.end_block_idx - 1 and ins.reduction_block_idx == 0
+    bs = globs.o_proj_block_size
+    r0 = ins.start_block_idx * bs
+    out = matvec(globs.o_proj_weights[ins.layer_idx], globs.attn_out, r0, bs)
+    globs.hidden_states[r0:r0 + bs] += out
+    globs.barriers[ins.layer_idx, ins.opcode() - 1, 0] += ins.end_block_idx - ins.start_block_idx
+
+
+LM_HEAD_REDUCTION = 2048
+
+
+def solve_lm_head(globs: MixtralGlobals, ins: Mixtral_RMS_LM_Head):
+    """mkm/python_vm.py:321-345: ``logits[rows] += bf16(W[rows, cols] @
+    post_ln[cols])`` over the 2048-column block ``reduction_block_idx``."""
+    bar = globs.barriers[globs.num_hidden_layers - 1, ExpertDownProjFused.opcode() - 1]
+    assert bar[0] == expected_downproj_barrier(globs), f"LM head: downproj barrier {int(bar[0])}"
+    post_ln = rms_norm(globs.hidden_states, globs.lm_head_norm_weights.reshape(-1).contiguous(), globs.rms_norm_eps)
+    c0 = ins.reduction_block_idx * LM_HEAD_REDUCTION
+    cols = slice(c0, c0 + LM_HEAD_REDUCTION)
+    w = globs.lm_head_weights[:, cols].contiguous()
+    vec = post_ln[cols].contiguous()
+    bs = globs.lm_head_block_size
+    for b in range(ins.start_output_block_idx, ins.end_output_block_idx):
+        r0 = b * bs
+        globs.logits[r0:r0 + bs] += matvec(w, vec, r0, bs)
+
+
 INSTRUCTION_TO_SOLVER = {
+    Mixtral_QKV: solve_qkv,
+    Mixtral_PartialAttn: solve_partial_attn,
+    Mixtral_AttnReduction: solve_attn_reduction,
+    Mixtral_OProj: solve_oproj,
     RmsRouterUpgate: solve_rms_router_upgate,
     ExpertDownProjFused: solve_expert_downproj_fused,
+    Mixtral_RMS_LM_Head: solve_lm_head,
     SpeculativeExpertPredict: solve_speculative_expert_predict,
 }
 
