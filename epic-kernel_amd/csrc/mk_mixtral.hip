@@ -38,6 +38,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <cstring>
 #include <mutex>
 #include <stddef.h>
 #include <stdint.h>
@@ -127,15 +128,21 @@ struct KParams {
     uint32_t timeout_ticks;
     int32_t *scratch;
     int32_t work_sharing;
-    // attention side and LM head (opcodes 1-4, 7); attn == 0 when absent
+    // attention side and LM head (opcodes 1-4, 7): attn == 0 when absent,
+    // else `ap` points at their parameters in device memory (read only by
+    // those opcodes, so the opcode-5/6 loops carry none of them)
     int32_t attn;
+    const struct AttnParams *ap;
+    uint32_t pos;  // pos_id: changes every decode step, so it stays a kernel argument
+};
+
+struct AttnParams {
     const uint16_t *qkv, *attn_ln, *oproj, *lm_norm, *lm_head;
     uint16_t *kc, *vc, *q_rope, *attn_out, *logits;
     const float *rope_cos, *rope_sin;
     float *lse_int, *out_int;
     int32_t Hq, Hkv, D, V, T, P;
     int32_t qkv_bs, kv_bs, lm_bs, lm_red;
-    uint32_t pos;
     float attn_scale;
     int32_t skip_red;
 };
@@ -1138,8 +1145,9 @@ __device__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int3
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
     if (!need_attention(p, c, 1, layer)) return false;
-    const int D = p.D, qkv_rows = (p.Hq + 2 * p.Hkv) * D;
-    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.qkv_bs > qkv_rows) {
+    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    const int D = a.D, qkv_rows = (a.Hq + 2 * a.Hkv) * D;
+    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * a.qkv_bs > qkv_rows) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 1, layer, b0, b1);
         return false;
     }
@@ -1147,40 +1155,40 @@ __device__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int3
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 1, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    rms_to_lds(p, sh, act, p.attn_ln + (size_t)layer * p.H);
+    rms_to_lds(p, sh, act, a.attn_ln + (size_t)layer * p.H);
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
-    const int r0 = b0 * p.qkv_bs, nrows = (b1 - b0) * p.qkv_bs;
+    const int r0 = b0 * a.qkv_bs, nrows = (b1 - b0) * a.qkv_bs;
     float *rowv = reinterpret_cast<float *>(act + (p.H >> 3));  // the block's outputs, bf16-rounded
-    matvec_rows(sh, p.qkv + (size_t)layer * qkv_rows * p.H, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
+    matvec_rows(sh, a.qkv + (size_t)layer * qkv_rows * p.H, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
                 [&](int r, float s) { rowv[r - r0] = rbf(s); });
     __syncthreads();
 
     // RoPE on q and k rows (interleaved pairs (2i, 2i+1) share cos/sin[2i]):
     // y = x * cos + rot(x) * sin in fp32 without contraction, rot(a, b) =
     // (-b, a); then q -> q_post_rope, k/v -> the caches at pos_id.
-    const int k0 = p.Hq * D, v0 = k0 + p.Hkv * D;
-    const size_t kv_base = ((size_t)layer * p.T + p.pos) * (size_t)(p.Hkv * D);
+    const int k0 = a.Hq * D, v0 = k0 + a.Hkv * D;
+    const size_t kv_base = ((size_t)layer * a.T + p.pos) * (size_t)(a.Hkv * D);
     for (int i = threadIdx.x; i < nrows; i += kThreads) {
         const int r = r0 + i;
         float y = rowv[i];
         if (r < v0) {
             const int d = r % D;
             const float partner = rowv[i ^ 1];
-            const float cs = p.rope_cos[(size_t)p.pos * D + d], sn = p.rope_sin[(size_t)p.pos * D + d];
+            const float cs = a.rope_cos[(size_t)p.pos * D + d], sn = a.rope_sin[(size_t)p.pos * D + d];
             y = __fadd_rn(__fmul_rn(y, cs), __fmul_rn((d & 1) ? partner : -partner, sn));
         }
         const uint32_t bits = f2bf(y);
         if (r < k0)
-            st_dev16(p.q_rope + r, bits);
+            st_dev16(a.q_rope + r, bits);
         else if (r < v0)
-            st_dev16(p.kc + kv_base + (r - k0), bits);
+            st_dev16(a.kc + kv_base + (r - k0), bits);
         else
-            st_dev16(p.vc + kv_base + (r - v0), bits);
+            st_dev16(a.vc + kv_base + (r - v0), bits);
     }
     drain_and_sync();
     // one arrival per block on its head's counter
-    const int bph = D / p.qkv_bs;
+    const int bph = D / a.qkv_bs;
     for (int b = b0 + (int)threadIdx.x; b < b1; b += kThreads)
         __hip_atomic_fetch_add(bar_at(p, layer, 1) + b / bph, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
@@ -1207,31 +1215,31 @@ __device__ __forceinline__ float wave_max(float v) {
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int GQA>
-__device__ bool partial_attn(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c, int layer, int kv,
-                             int nparts, int pidx, int32_t *tim) {
+__device__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState &sh, u32x4 *act, const Ctx &c,
+                             int layer, int kv, int nparts, int pidx, int32_t *tim) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int D = p.D, G = D / 8, TPW = 64 / G;
+    const int D = a.D, G = D / 8, TPW = 64 / G;
     const int slot = lane / G, dp = lane % G;
     const int h0 = kv * GQA;
 
     // producers: the GQA query heads, the key head and the value head
-    const int bph = D / p.qkv_bs;
+    const int bph = D / a.qkv_bs;
     const int32_t *bar_qkv = bar_at(p, layer, 1);
-    const int32_t *mine = bar_qkv + (lane < GQA ? h0 + lane : lane == GQA ? p.Hq + kv : p.Hq + p.Hkv + kv);
+    const int32_t *mine = bar_qkv + (lane < GQA ? h0 + lane : lane == GQA ? a.Hq + kv : a.Hq + a.Hkv + kv);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_lanes_ge(p, sh, mine, GQA + 2, bph, c, 2, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
     const int seq = (int)p.pos + 1;
-    const int total = (seq + p.kv_bs - 1) / p.kv_bs;
+    const int total = (seq + a.kv_bs - 1) / a.kv_bs;
     const int per = (total + nparts - 1) / nparts;
     const int tb0 = pidx * per, tb1 = min(tb0 + per, total);
-    const int t0 = tb0 * p.kv_bs, t1 = min(tb1 * p.kv_bs, seq);
+    const int t0 = tb0 * a.kv_bs, t1 = min(tb1 * a.kv_bs, seq);
 
     float q[GQA][8];
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
-        const u32x4 qv = ld_dev128(p.q_rope, (uint32_t)(((h0 + h) * D + dp * 8) * 2));
+        const u32x4 qv = ld_dev128(a.q_rope, (uint32_t)(((h0 + h) * D + dp * 8) * 2));
         const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1248,9 +1256,9 @@ __device__ bool partial_attn(const KParams &p, SharedState &sh, u32x4 *act, cons
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
     }
     // K and V of this layer and KV head: position t at byte (t * Hkv * D) * 2
-    const uint16_t *kbase = p.kc + (size_t)layer * p.T * p.Hkv * D + (size_t)kv * D;
-    const uint16_t *vbase = p.vc + (size_t)layer * p.T * p.Hkv * D + (size_t)kv * D;
-    const uint32_t row_bytes = (uint32_t)(p.Hkv * D * 2);
+    const uint16_t *kbase = a.kc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
+    const uint16_t *vbase = a.vc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
+    const uint32_t row_bytes = (uint32_t)(a.Hkv * D * 2);
     const int steps = (t1 - t0 + TPW - 1) / TPW;  // <= 0 for an empty partition
     for (int st = wave; st < steps; st += kWaves) {
         const int t = t0 + st * TPW + slot;
@@ -1268,7 +1276,7 @@ __device__ bool partial_attn(const KParams &p, SharedState &sh, u32x4 *act, cons
                 s = fmaf(q[h][2 * j], bf2f(kw[j] & 0xffffu), s);
                 s = fmaf(q[h][2 * j + 1], bf2f(kw[j] >> 16), s);
             }
-            s = group_sum(s, G) * p.attn_scale;
+            s = group_sum(s, G) * a.attn_scale;
             if (!valid) s = -INFINITY;
             const float mn = fmaxf(m[h], wave_max(s));  // finite: the step has a valid token
             const float alpha = expf(m[h] - mn);        // 0 while m is -inf
@@ -1325,18 +1333,18 @@ __device__ bool partial_attn(const KParams &p, SharedState &sh, u32x4 *act, cons
             }
         }
         const float out = L > 0.f ? O / L : 0.f;
-        if (p.skip_red) {
-            st_dev16(p.attn_out + (h0 + h) * D + d, f2bf(out));
+        if (a.skip_red) {
+            st_dev16(a.attn_out + (h0 + h) * D + d, f2bf(out));
         } else {
-            st_dev32(p.out_int + ((size_t)(h0 + h) * p.P + pidx) * D + d, __float_as_uint(out));
+            st_dev32(a.out_int + ((size_t)(h0 + h) * a.P + pidx) * D + d, __float_as_uint(out));
             if (d == 0) {
                 const float lse = L > 0.f ? log2f(L) + M * kLog2e : -INFINITY;
-                st_dev32(p.lse_int + (size_t)(h0 + h) * p.P + pidx, __float_as_uint(lse));
+                st_dev32(a.lse_int + (size_t)(h0 + h) * a.P + pidx, __float_as_uint(lse));
             }
         }
     }
     drain_and_sync();
-    if (p.skip_red)
+    if (a.skip_red)
         arrive(bar_at(p, layer, 3), GQA);
     else if (threadIdx.x < GQA)
         __hip_atomic_fetch_add(bar_at(p, layer, 2) + h0 + threadIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1351,15 +1359,16 @@ __device__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, c
     const int nparts = __builtin_amdgcn_readfirstlane(ins[3]);
     const int pidx = __builtin_amdgcn_readfirstlane(ins[4]);
     if (!need_attention(p, c, 2, layer)) return false;
-    if (layer < 0 || layer >= p.num_layers || kv < 0 || kv >= p.Hkv || nparts < 1 || pidx < 0 || pidx >= nparts ||
-        (!p.skip_red && pidx >= p.P)) {
+    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    if (layer < 0 || layer >= p.num_layers || kv < 0 || kv >= a.Hkv || nparts < 1 || pidx < 0 || pidx >= nparts ||
+        (!a.skip_red && pidx >= a.P)) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 2, layer, kv, pidx);
         return false;
     }
-    switch (p.Hq / p.Hkv) {
-    case 1: return partial_attn<1>(p, sh, act, c, layer, kv, nparts, pidx, tim);
-    case 2: return partial_attn<2>(p, sh, act, c, layer, kv, nparts, pidx, tim);
-    default: return partial_attn<4>(p, sh, act, c, layer, kv, nparts, pidx, tim);
+    switch (a.Hq / a.Hkv) {
+    case 1: return partial_attn<1>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
+    case 2: return partial_attn<2>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
+    default: return partial_attn<4>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
     }
 }
 
@@ -1373,13 +1382,14 @@ __device__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32
     const int terminal = __builtin_amdgcn_readfirstlane(ins[4]);
     const int n = __builtin_amdgcn_readfirstlane(ins[5]);
     if (!need_attention(p, c, 3, layer)) return false;
-    const int gqa = p.Hq / p.Hkv;
+    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    const int gqa = a.Hq / a.Hkv;
     const int out_slot = (n >= 0 && n <= MK_INTS_PER_INSTRUCTION - 7) ? __builtin_amdgcn_readfirstlane(ins[6 + n]) : -1;
-    bool bad = layer < 0 || layer >= p.num_layers || hs < 0 || hs + gqa > p.Hq || n < 1 ||
-               n > MK_INTS_PER_INSTRUCTION - 7 || (!terminal && (out_slot < 0 || out_slot >= p.P));
+    bool bad = layer < 0 || layer >= p.num_layers || hs < 0 || hs + gqa > a.Hq || n < 1 ||
+               n > MK_INTS_PER_INSTRUCTION - 7 || (!terminal && (out_slot < 0 || out_slot >= a.P));
     for (int i = 0; !bad && i < n; ++i) {
         const int s = ins[6 + i];
-        bad = s < 0 || s >= p.P;
+        bad = s < 0 || s >= a.P;
     }
     if (bad) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 3, layer, hs, n);
@@ -1388,24 +1398,24 @@ __device__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 2) + hs, nparts, c, 3, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    const int D = p.D;
+    const int D = a.D;
     for (int i = threadIdx.x; i < gqa * D; i += kThreads) {
         const int h = hs + i / D, d = i % D;
         float M = -INFINITY;
-        for (int k = 0; k < n; ++k) M = fmaxf(M, __uint_as_float(ld_dev32(p.lse_int + (size_t)h * p.P + ins[6 + k])));
+        for (int k = 0; k < n; ++k) M = fmaxf(M, __uint_as_float(ld_dev32(a.lse_int + (size_t)h * a.P + ins[6 + k])));
         float den = 0.f, num = 0.f;
         for (int k = 0; k < n; ++k) {
             const int s = ins[6 + k];
-            const float f = exp2f(__uint_as_float(ld_dev32(p.lse_int + (size_t)h * p.P + s)) - M);
+            const float f = exp2f(__uint_as_float(ld_dev32(a.lse_int + (size_t)h * a.P + s)) - M);
             den += f;
-            num += __uint_as_float(ld_dev32(p.out_int + ((size_t)h * p.P + s) * D + d)) * f;
+            num += __uint_as_float(ld_dev32(a.out_int + ((size_t)h * a.P + s) * D + d)) * f;
         }
         const float red = num / den;
         if (terminal) {
-            st_dev16(p.attn_out + h * D + d, f2bf(red));
+            st_dev16(a.attn_out + h * D + d, f2bf(red));
         } else {
-            st_dev32(p.out_int + ((size_t)h * p.P + out_slot) * D + d, __float_as_uint(red));
-            if (d == 0) st_dev32(p.lse_int + (size_t)h * p.P + out_slot, __float_as_uint(logf(den)));
+            st_dev32(a.out_int + ((size_t)h * a.P + out_slot) * D + d, __float_as_uint(red));
+            if (d == 0) st_dev32(a.lse_int + (size_t)h * a.P + out_slot, __float_as_uint(logf(den)));
         }
     }
     drain_and_sync();
@@ -1423,19 +1433,20 @@ __device__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const in
     const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
     const int red = __builtin_amdgcn_readfirstlane(ins[4]);
     if (!need_attention(p, c, 4, layer)) return false;
+    const AttnParams &a = *p.ap;  // valid: attention tensors are present
     if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.oproj_bs > p.H || red != 0) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 4, layer, b0, b1);
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 3), p.Hq, c, 4, layer)) return false;
+    if (!wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    const int K = p.Hq * p.D;  // reduction length
-    for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(p.attn_out, (uint32_t)v * 16u);
+    const int K = a.Hq * a.D;  // reduction length
+    for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(a.attn_out, (uint32_t)v * 16u);
     __syncthreads();
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    matvec_rows(sh, p.oproj + (size_t)layer * p.H * K, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs,
+    matvec_rows(sh, a.oproj + (size_t)layer * p.H * K, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs,
                 (b1 - b0) * p.oproj_bs, [&](int r, float s) {
                     uint16_t *hp = p.hidden + r;
                     st_dev16(hp, f2bf(bf2f(ld_dev16(hp)) + rbf(s)));
@@ -1457,7 +1468,8 @@ __device__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const 
     const int red = __builtin_amdgcn_readfirstlane(ins[3]);
     const int last = p.num_layers - 1;
     if (!need_attention(p, c, 7, last)) return false;
-    if (b0 < 0 || b1 < b0 || (int64_t)b1 * p.lm_bs > p.V || red < 0 || (int64_t)(red + 1) * p.lm_red > p.H) {
+    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    if (b0 < 0 || b1 < b0 || (int64_t)b1 * a.lm_bs > a.V || red < 0 || (int64_t)(red + 1) * a.lm_red > p.H) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 7, last, b0, b1);
         return false;
     }
@@ -1465,24 +1477,24 @@ __device__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const 
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, last, 6), 2 * (p.H / p.down_bs), c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    rms_to_lds(p, sh, act, p.lm_norm);
+    rms_to_lds(p, sh, act, a.lm_norm);
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     // logits[r] += bf16(W[r, cols] . normed[cols]) for a pair of rows at a
     // time: one packed bf16 atomic add per pair (rows are even-aligned)
-    const int col0 = red * p.lm_red;
+    const int col0 = red * a.lm_red;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = b0 * p.lm_bs, nrows = (b1 - b0) * p.lm_bs;
+    const int r0 = b0 * a.lm_bs, nrows = (b1 - b0) * a.lm_bs;
     for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
         const int ra = r0 + 2 * it;
         float aa = 0.f, ab = 0.f;
-        dot_pair(p.lm_head + (size_t)ra * p.H + col0, p.lm_head + (size_t)(ra + 1) * p.H + col0, act + (col0 >> 3),
-                 act + (col0 >> 3), p.lm_red / kChunkElems, lane, aa, ab);
+        dot_pair(a.lm_head + (size_t)ra * p.H + col0, a.lm_head + (size_t)(ra + 1) * p.H + col0, act + (col0 >> 3),
+                 act + (col0 >> 3), a.lm_red / kChunkElems, lane, aa, ab);
         aa = wave_sum(aa);
         ab = wave_sum(ab);
         if (lane == 0) {
             const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(aa)), __builtin_bit_cast(__bf16, (uint16_t)f2bf(ab))};
             __builtin_amdgcn_global_atomic_fadd_v2bf16(
-                (__attribute__((address_space(1))) bf16x2_t *)(p.logits + ra), v);
+                (__attribute__((address_space(1))) bf16x2_t *)(a.logits + ra), v);
         }
     }
     drain_and_sync();
@@ -1494,7 +1506,11 @@ __device__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const 
 // the persistent interpreter
 // ---------------------------------------------------------------------------
 
-template <int kE>
+// kAttn: whether opcodes 1-4 and 7 are compiled in.  The MoE-only variant
+// keeps the register allocation of the opcode 5/6 streaming loops free of
+// the attention code's live ranges; launches without attention tensors use
+// it.
+template <int kE, bool kAttn>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
@@ -1512,14 +1528,24 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         bool ok = true;
         switch (op) {
         case 0: break;
-        case 1: ok = op_qkv(p, sh, act, ins, c, tim); break;
-        case 2: ok = op_partial_attn(p, sh, act, ins, c, tim); break;
-        case 3: ok = op_attn_reduction(p, sh, ins, c, tim); break;
-        case 4: ok = op_oproj(p, sh, act, ins, c, tim); break;
         case 5: ok = op_rms_router_upgate<kE>(p, sh, act, ins, c, tim); break;
         case 6: ok = op_expert_downproj(p, sh, act, ins, c, tim); break;
-        case 7: ok = op_lm_head(p, sh, act, ins, c, tim); break;
         case 8: ok = op_predict<kE>(p, sh, act, ins, c, tim); break;
+        case 1:
+        case 2:
+        case 3:
+        case 4:
+        case 7:
+            if constexpr (kAttn) {
+                if (op == 1) ok = op_qkv(p, sh, act, ins, c, tim);
+                else if (op == 2) ok = op_partial_attn(p, sh, act, ins, c, tim);
+                else if (op == 3) ok = op_attn_reduction(p, sh, ins, c, tim);
+                else if (op == 4) ok = op_oproj(p, sh, act, ins, c, tim);
+                else ok = op_lm_head(p, sh, act, ins, c, tim);
+            } else {
+                ok = need_attention(p, c, op, __builtin_amdgcn_readfirstlane(ins[1]));
+            }
+            break;
         default:
             report_error(p, MK_ERR_BAD_OPCODE, c, op, 0, 0, op);
             ok = false;
@@ -1559,6 +1585,8 @@ struct DeviceState {
     int32_t *status = nullptr;
     int32_t *scratch = nullptr;
     size_t scratch_ints = 0;
+    AttnParams *attn = nullptr;  // attention parameters of the launches that have them
+    AttnParams attn_host{};      // what `attn` holds (after the stream reaches the copy)
 };
 
 std::mutex g_mutex;
@@ -1721,7 +1749,7 @@ int mk_mixtral_query_device(int device, int32_t *num_cus, int32_t *max_workers) 
     if (rc != MK_OK) return rc;
     int blocks = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &blocks, reinterpret_cast<const void *>(mk_mixtral_kernel<0>), kThreads, kMinLdsBytes);
+        &blocks, reinterpret_cast<const void *>(mk_mixtral_kernel<0, true>), kThreads, kMinLdsBytes);
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (num_cus) *num_cus = st->num_cus;
     if (max_workers) *max_workers = blocks * st->num_cus;
@@ -1743,8 +1771,11 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     int blocks = 0;
     // Mixtral's 8 experts get a kernel specialised for exactly 8
     const bool e8 = g->num_experts == 8;
-    const void *fn = e8 ? reinterpret_cast<const void *>(mk_mixtral_kernel<8>)
-                        : reinterpret_cast<const void *>(mk_mixtral_kernel<0>);
+    const bool attn = g->qkv_weights != nullptr;
+    const void *fn = e8 ? (attn ? reinterpret_cast<const void *>(mk_mixtral_kernel<8, true>)
+                                : reinterpret_cast<const void *>(mk_mixtral_kernel<8, false>))
+                        : (attn ? reinterpret_cast<const void *>(mk_mixtral_kernel<0, true>)
+                                : reinterpret_cast<const void *>(mk_mixtral_kernel<0, false>));
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds);
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (g->num_workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
@@ -1805,40 +1836,59 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.scratch = st->scratch;
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.attn = g->qkv_weights != nullptr;
-    kp.qkv = g->qkv_weights;
-    kp.attn_ln = g->attn_norm_weights;
-    kp.oproj = g->o_weights;
-    kp.lm_norm = g->lm_head_norm_weights;
-    kp.lm_head = g->lm_head_weights;
-    kp.kc = g->k_cache;
-    kp.vc = g->v_cache;
-    kp.q_rope = g->q_post_rope;
-    kp.attn_out = g->attn_out;
-    kp.logits = g->logits;
-    kp.rope_cos = g->rope_cos;
-    kp.rope_sin = g->rope_sin;
-    kp.lse_int = g->attn_lse_intermediates;
-    kp.out_int = g->attn_out_intermediates;
-    kp.Hq = g->num_attention_heads;
-    kp.Hkv = g->num_kv_heads;
-    kp.D = g->head_dim;
-    kp.V = g->vocab_size;
-    kp.T = g->kv_capacity;
-    kp.P = g->attn_partial_slots;
-    kp.qkv_bs = g->qkv_block_size;
-    kp.kv_bs = g->attn_kv_block_size;
-    kp.lm_bs = g->lm_head_block_size;
-    kp.lm_red = g->lm_head_reduction;
+    kp.ap = nullptr;
+    if (kp.attn) {
+        AttnParams a{};
+        a.qkv = g->qkv_weights;
+        a.attn_ln = g->attn_norm_weights;
+        a.oproj = g->o_weights;
+        a.lm_norm = g->lm_head_norm_weights;
+        a.lm_head = g->lm_head_weights;
+        a.kc = g->k_cache;
+        a.vc = g->v_cache;
+        a.q_rope = g->q_post_rope;
+        a.attn_out = g->attn_out;
+        a.logits = g->logits;
+        a.rope_cos = g->rope_cos;
+        a.rope_sin = g->rope_sin;
+        a.lse_int = g->attn_lse_intermediates;
+        a.out_int = g->attn_out_intermediates;
+        a.Hq = g->num_attention_heads;
+        a.Hkv = g->num_kv_heads;
+        a.D = g->head_dim;
+        a.V = g->vocab_size;
+        a.T = g->kv_capacity;
+        a.P = g->attn_partial_slots;
+        a.qkv_bs = g->qkv_block_size;
+        a.kv_bs = g->attn_kv_block_size;
+        a.lm_bs = g->lm_head_block_size;
+        a.lm_red = g->lm_head_reduction;
+        a.attn_scale = g->attn_scale;
+        a.skip_red = g->skip_attn_reduction ? 1 : 0;
+        if (st->attn == nullptr) {
+            std::lock_guard<std::mutex> lock(g_mutex);
+            if (st->attn == nullptr &&
+                (e = hipMalloc(reinterpret_cast<void **>(&st->attn), sizeof(AttnParams))) != hipSuccess)
+                return hip_fail(e, "hipMalloc");
+        }
+        // Copied only when it changes (a decode loop launches the same
+        // tensors every step); stream-ordered after the launches that read
+        // the previous contents.
+        if (std::memcmp(&a, &st->attn_host, sizeof(a)) != 0) {
+            if ((e = hipMemcpyAsync(st->attn, &a, sizeof(a), hipMemcpyHostToDevice,
+                                    reinterpret_cast<hipStream_t>(stream))) != hipSuccess)
+                return hip_fail(e, "hipMemcpyAsync");
+            st->attn_host = a;
+        }
+        kp.ap = st->attn;
+    }
     kp.pos = g->pos_id;
-    kp.attn_scale = g->attn_scale;
-    kp.skip_red = g->skip_attn_reduction ? 1 : 0;
 
-    if (e8)
-        hipLaunchKernelGGL(mk_mixtral_kernel<8>, dim3((unsigned)g->num_workers), dim3(kThreads), lds,
-                           reinterpret_cast<hipStream_t>(stream), kp);
-    else
-        hipLaunchKernelGGL(mk_mixtral_kernel<0>, dim3((unsigned)g->num_workers), dim3(kThreads), lds,
-                           reinterpret_cast<hipStream_t>(stream), kp);
+    // fn is one of the four instantiations above
+    void *args[] = {&kp};
+    e = hipLaunchKernel(fn, dim3((unsigned)g->num_workers), dim3(kThreads), args, lds,
+                        reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel");
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "hipGetLastError");
     return MK_OK;
