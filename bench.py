@@ -226,6 +226,100 @@ def record_trace(bench, path: str, launches: int = 8):
     print(format_report(rec), file=sys.stderr, flush=True)
 
 
+def decode_bytes_per_token(cfg, seq_len: int) -> int:
+    """Algorithmic HBM bytes of one whole-model decode step: every layer's
+    attention weights, norms, router and the two selected experts, the K and
+    V rows of all cached positions, and the LM head with its norm (bf16)."""
+    L, H, F, E, k = (cfg.num_hidden_layers, cfg.hidden_size, cfg.intermediate_size, cfg.num_local_experts,
+                     cfg.num_experts_per_tok)
+    Hq, Hkv, D, V = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.vocab_size
+    attn = (Hq + 2 * Hkv) * D * H + H * Hq * D + H
+    moe = E * H + H + k * 3 * F * H
+    kv = 2 * seq_len * Hkv * D
+    return 2 * (L * (attn + moe + kv) + V * H + H)
+
+
+def decode_bench(args):
+    """Whole-model greedy decode (BASELINE configs 4 and 5) through
+    MK_Generator: random-init Mixtral-8x7B-shaped weights resident in HBM,
+    a KV cache pre-filled with N(0, 1) to the context length, `decode_steps`
+    timed steps after `warmup` untimed ones."""
+    import torch
+
+    from megakernels_amd.mixtral.generate import MK_Generator
+    from megakernels_amd.mixtral.synthetic import C4, make_synthetic_mixtral
+
+    cfg = C4
+    prefill = 4096 if args.config == "c4" else 16384
+    steps, warmup = args.decode_steps, max(1, args.warmup)
+    print(f"bench: building {args.config} ({cfg.num_hidden_layers} layers, {prefill} cached positions) on cuda:0",
+          file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    model = make_synthetic_mixtral(cfg, "cuda", 0, full=True, kv_positions=prefill + steps + warmup + 1,
+                                   prefill=prefill, predictor_sigma=args.predict_sigma)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    gen = MK_Generator.build(model, prefill)
+    print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
+          f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
+    tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
+    import mk_mixtral
+
+    mk_mixtral.raise_if_failed("cuda")
+    if args.trace:
+        from megakernels_amd.trace import TimingRecord, format_report, save_record
+
+        gen.launch_kwargs["record_timings"] = True
+        g0 = gen.schedule.globs
+        g0.timings.zero_()
+        gen.run(tokens[:, -1:], pos_id=prefill + steps)
+        torch.cuda.synchronize()
+        gen.launch_kwargs.pop("record_timings")
+        rec = TimingRecord.from_globals(g0)
+        save_record(args.trace, rec)
+        print(format_report(rec), file=sys.stderr, flush=True)
+    ms = secs / steps * 1e3
+    nbytes = decode_bytes_per_token(cfg, prefill + steps // 2)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    g = gen.schedule.globs
+    out = {
+        "metric": METRIC,
+        "value": steps / secs,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"BASELINE config {'4' if args.config == 'c4' else '5'}: Mixtral-8x7B-shaped batch-1 greedy "
+                        f"decode (32 layers, 32/8 heads, head dim 128, 8 experts top-2, vocab 32000), KV cache "
+                        f"pre-filled to {prefill} positions, one persistent-kernel launch per token",
+            "prefill": prefill,
+            "workers": g.sm_count(),
+            "attention_partitions": int(max(i.num_partials for i in gen.schedule.get_linear_instructions()
+                                            if i.opcode() == 2)),
+            "predictor_sigma": args.predict_sigma,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "bytes_per_launch": nbytes,
+            "kernel": "mk_mixtral_kernel (whole model)",
+        },
+        "tokens_tail": tokens[0, -8:].tolist(),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def cpu_baseline(bench, seconds: float, threads: int):
     """The CPU oracle (restated python_vm, C + OpenMP) on the same weights,
     inputs and instruction list, over a bounded sample of tokens."""
@@ -288,7 +382,12 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=1024)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c4", "c5"],
+                    help="c1/c2: one MoE layer per launch (c2 is the headline); c4/c5: whole-model greedy "
+                         "decode of the Mixtral-8x7B shape with 4096 / 16384 cached positions")
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--predict-sigma", type=float, default=None,
+                    help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
     ap.add_argument("--no-skewed", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
@@ -323,6 +422,10 @@ def main():
         return
 
     from megakernels_amd.mixtral.synthetic import C1, C2
+
+    if args.config in ("c4", "c5"):
+        decode_bench(args)
+        return
 
     cfg = C2 if args.config == "c2" else C1
     print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)

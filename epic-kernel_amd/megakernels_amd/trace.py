@@ -62,6 +62,10 @@ class TimingRecord:
     expert_proj_block_size: int
     down_proj_block_size: int
     k: int = 2
+    qkv_block_size: int = 0
+    o_proj_block_size: int = 0
+    lm_head_block_size: int = 0
+    attn_width: int = 0  # Hq * head_dim, the O-projection's reduction length
 
     @classmethod
     def from_globals(cls, globs) -> "TimingRecord":
@@ -74,6 +78,10 @@ class TimingRecord:
             expert_proj_block_size=globs.expert_proj_block_size,
             down_proj_block_size=globs.down_proj_block_size,
             k=globs.num_experts_per_tok,
+            qkv_block_size=globs.qkv_block_size,
+            o_proj_block_size=globs.o_proj_block_size,
+            lm_head_block_size=globs.lm_head_block_size,
+            attn_width=globs.num_attention_heads * globs.head_dim,
         )
 
     def micros(self) -> np.ndarray:
@@ -110,6 +118,12 @@ class TimingRecord:
             return self.k * rows * F * 2
         if op == 8:
             return E * H * 2 + H * 2
+        if op == 1 and self.qkv_block_size:
+            return (int(ins[3]) - int(ins[2])) * self.qkv_block_size * H * 2
+        if op == 4 and self.o_proj_block_size:
+            return (int(ins[3]) - int(ins[2])) * self.o_proj_block_size * self.attn_width * 2
+        if op == 7 and self.lm_head_block_size:
+            return (int(ins[2]) - int(ins[1])) * self.lm_head_block_size * 2048 * 2
         return 0
 
 
@@ -117,13 +131,15 @@ def save_record(path, rec: TimingRecord) -> None:
     np.savez_compressed(
         path, timings=rec.timings, instructions=rec.instructions,
         shape=np.array([rec.hidden_size, rec.intermediate_size, rec.num_experts,
-                        rec.expert_proj_block_size, rec.down_proj_block_size, rec.k]))
+                        rec.expert_proj_block_size, rec.down_proj_block_size, rec.k,
+                        rec.qkv_block_size, rec.o_proj_block_size, rec.lm_head_block_size, rec.attn_width]))
 
 
 def load_record(path) -> TimingRecord:
     d = np.load(Path(path), allow_pickle=False)
-    H, F, E, ebs, dbs, k = (int(x) for x in d["shape"])
-    return TimingRecord(d["timings"], d["instructions"], H, F, E, ebs, dbs, k)
+    shape = [int(x) for x in d["shape"]] + [0] * 4
+    H, F, E, ebs, dbs, k, qbs, obs, lbs, aw = shape[:10]
+    return TimingRecord(d["timings"], d["instructions"], H, F, E, ebs, dbs, k, qbs, obs, lbs, aw)
 
 
 def barrier_waits(rec: TimingRecord) -> dict:
@@ -206,6 +222,27 @@ def phase_summary(rec: TimingRecord, percentiles=(0, 10, 50, 90, 100)) -> dict:
     return out
 
 
+def stage_windows(rec: TimingRecord) -> dict:
+    """Per (layer, opcode): (first start, last end, last completion) in us --
+    the critical-path view of a whole-model step (the LM head is layer -1)."""
+    t = rec.micros()
+    ops = rec.instructions[:, :, 0]
+    layers = rec.instructions[:, :, 1]
+    out: dict = {}
+    W, Q = ops.shape
+    for w in range(W):
+        for q in range(Q):
+            op = int(ops[w, q])
+            if op == 0 or np.isnan(t[w, q, T_START]):
+                continue
+            key = (-1 if op == 7 else int(layers[w, q]), op)
+            a, b = t[w, q, T_START], t[w, q, T_END]
+            done = t[w, q, T_DONE_STORE]
+            lo, hi, dn = out.get(key, (np.inf, -np.inf, -np.inf))
+            out[key] = (min(lo, a), max(hi, b), max(dn, done if not np.isnan(done) else b))
+    return out
+
+
 def format_report(rec: TimingRecord, peak_gbs: float = 8000.0) -> str:
     """A plain-text report of the three analyses."""
     lines = []
@@ -219,6 +256,17 @@ def format_report(rec: TimingRecord, peak_gbs: float = 8000.0) -> str:
         lines.append(f"streamed {total / 1e6:.1f} MB over {starts[busy][-1] - starts[busy][0] + 1:.0f} us; "
                      f"peak bin {gbs.max():.0f} GB/s ({frac.max():.1%}), mean over busy bins "
                      f"{gbs[busy].mean():.0f} GB/s ({frac[busy].mean():.1%})")
+    win = stage_windows(rec)
+    layers = sorted({lay for lay, _ in win if lay >= 0})
+    if len(layers) > 1:
+        show = layers[len(layers) // 2]
+        lines.append(f"layer {show} stage windows (us, first start / last end):")
+        for (lay, op), (a, b, _) in sorted(win.items()):
+            if lay == show:
+                lines.append(f"  {OPCODE_NAMES.get(op, op):26s} {a:9.1f} {b:9.1f}  ({b - a:6.1f})")
+        ends = [max(b for (lay, _), (_, b, _) in win.items() if lay == L) for L in layers]
+        if len(ends) > 2:
+            lines.append(f"mean layer period {np.mean(np.diff(ends)):.1f} us over {len(layers)} layers")
     lines.append("event percentiles (us): p0 p10 p50 p90 p100")
     for (name, ev), v in phase_summary(rec).items():
         lines.append(f"  {name:26s} {ev:10s} " + " ".join(f"{x:7.1f}" for x in v))
