@@ -145,6 +145,7 @@ struct AttnParams {
     int32_t qkv_bs, kv_bs, lm_bs, lm_red;
     float attn_scale;
     int32_t skip_red;
+    int32_t kv_ring;  // opcode-2 LDS ring chunks (1 .. kKvRingMax)
 };
 
 // Per-workgroup state that outlives a single instruction.
@@ -305,7 +306,7 @@ __device__ __forceinline__ bool aborted(const KParams &p) {
 }
 
 // Record the first failure; called by one lane.
-__device__ void report_error_lane(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected,
+__device__ __forceinline__ void report_error_lane(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected,
                                   int seen) {
     int zero = 0;
     if (__hip_atomic_compare_exchange_strong(p.status, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
@@ -320,13 +321,13 @@ __device__ void report_error_lane(const KParams &p, int code, const Ctx &c, int 
 }
 
 // Record the first failure (thread 0 of the reporting workgroup only).
-__device__ void report_error(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected, int seen) {
+__device__ __forceinline__ void report_error(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected, int seen) {
     if (threadIdx.x == 0) report_error_lane(p, code, c, opcode, layer, expected, seen);
 }
 
 // Wait until *ctr >= expected.  Thread 0 spins; the result is broadcast.
 // Returns false (uniformly) on time-out or when another worker has failed.
-__device__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int expected, const Ctx &c, int opcode,
+__device__ __forceinline__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int expected, const Ctx &c, int opcode,
                         int layer) {
     if (threadIdx.x == 0) {
         int ok = 1;
@@ -465,7 +466,7 @@ __device__ __forceinline__ float sumsq8(u32x4 x) { return sumsq2(x.x) + sumsq2(x
 // sums the per-wave partials itself, so the logits end up in registers after
 // a single workgroup barrier.
 template <int kE>
-__device__ void finish_logits(const KParams &p, SharedState &sh, const float *acc, float *logits) {
+__device__ __forceinline__ void finish_logits(const KParams &p, SharedState &sh, const float *acc, float *logits) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int e = 0; e < Experts<kE>::kMax; ++e) {
@@ -490,7 +491,7 @@ __device__ void finish_logits(const KParams &p, SharedState &sh, const float *ac
 // normed hidden (bf16) -> act[0 .. H/8); router logits -> logits[0 .. E) in
 // every thread.  Reads hidden_states, so it runs after the producer wait.
 template <int kE>
-__device__ void rms_router(const KParams &p, SharedState &sh, u32x4 *act, int layer, const uint16_t *router,
+__device__ __forceinline__ void rms_router(const KParams &p, SharedState &sh, u32x4 *act, int layer, const uint16_t *router,
                            const RouterRegs<kE> &rr, int32_t *tim, float *logits) {
     const int tid = threadIdx.x;
     const int nv = p.H >> 3;
@@ -545,7 +546,7 @@ struct Top2 {
 // comparison: the lower expert index wins a tie); p_i = exp(l_i - max) / sum
 // as torch.softmax computes it.
 template <int kE>
-__device__ Top2 softmax_top2(const KParams &p, const float *logits) {
+__device__ __forceinline__ Top2 softmax_top2(const KParams &p, const float *logits) {
     int i0 = 0;
     float l0 = logits[0];
 #pragma unroll
@@ -616,7 +617,7 @@ __device__ __forceinline__ int claim_issue(int32_t *cursor, int lane) {
 // slot) order, so every member enumerates the pooled items identically.
 // Instructions with out-of-range operands are left out (their owner reports
 // them).  Ends with a workgroup barrier.
-__device__ void pool_scan(const KParams &p, SharedState &sh, int layer, int group) {
+__device__ __forceinline__ void pool_scan(const KParams &p, SharedState &sh, int layer, int group) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int w0 = group * kPoolGroup;
     const int w1 = min((int)gridDim.x, w0 + kPoolGroup);
@@ -667,7 +668,7 @@ __device__ __forceinline__ int32_t *slot_cursor(const KParams &p, int slot) {
 // start at row0 (nrows rows, items 0 .. 2*nrows), claimed one at a time from
 // the instruction's cursor (the next claim is issued before the current
 // item's loads) until the cursor passes count.  Returns the number done here.
-__device__ int upgate_claimed(const KParams &p, const u32x4 *act, int layer, int row0, int nrows, int e0, int e1,
+__device__ __forceinline__ int upgate_claimed(const KParams &p, const u32x4 *act, int layer, int row0, int nrows, int e0, int e1,
                               int first, int count, int32_t *cursor, int lane) {
     int done_here = 0;
     int c = __builtin_amdgcn_readfirstlane(claim_issue(cursor, lane));
@@ -706,7 +707,7 @@ __device__ __forceinline__ void publish_items(const KParams &p, int32_t *done, i
 // spreads the waves), claims from it until it is exhausted, and repeats.
 // Routing is a function of the layer's inputs only, so the experts are the
 // owner's.
-__device__ void steal_upgate(const KParams &p, const SharedState &sh, const u32x4 *act, int layer, int self_k,
+__device__ __forceinline__ void steal_upgate(const KParams &p, const SharedState &sh, const u32x4 *act, int layer, int self_k,
                              int e0, int e1, int lane, int wave) {
     const int n = sh.pool_n;
     const int start = (self_k + 1 + wave) % n;
@@ -729,7 +730,7 @@ __device__ void steal_upgate(const KParams &p, const SharedState &sh, const u32x
 }
 
 template <int kE>
-__device__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
                                      const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -891,7 +892,7 @@ __device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 
     return acc;
 }
 
-__device__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
                                    const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1027,7 +1028,7 @@ __device__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act
 // ---------------------------------------------------------------------------
 
 template <int kE>
-__device__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     if (layer < 0 || layer >= p.num_layers) {
@@ -1068,7 +1069,7 @@ __device__ __forceinline__ bool need_attention(const KParams &p, const Ctx &c, i
 // Wait until the counter each of the first n (<= 64) lanes of wave 0 points
 // at reaches `expected`.  Every control value is wave-uniform (ballot,
 // readfirstlane); the result is broadcast to the workgroup like wait_ge's.
-__device__ bool wait_lanes_ge(const KParams &p, SharedState &sh, const int32_t *mine, int n, int expected,
+__device__ __forceinline__ bool wait_lanes_ge(const KParams &p, SharedState &sh, const int32_t *mine, int n, int expected,
                               const Ctx &c, int opcode, int layer) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
@@ -1104,7 +1105,7 @@ __device__ bool wait_lanes_ge(const KParams &p, SharedState &sh, const int32_t *
 // act[0 .. H/8) = bf16(w * bf16(h * 1/sqrt(mean(h^2) + eps))) of the current
 // hidden state (python_vm rms_norm, lat/python_vm.py:50-56).  Ends with a
 // workgroup barrier.
-__device__ void rms_to_lds(const KParams &p, SharedState &sh, u32x4 *act, const uint16_t *w) {
+__device__ __forceinline__ void rms_to_lds(const KParams &p, SharedState &sh, u32x4 *act, const uint16_t *w) {
     const int tid = threadIdx.x, nv = p.H >> 3;
     float ss = 0.f;
     for (int v = tid; v < nv; v += kThreads) ss += sumsq8(ld_dev128(p.hidden, (uint32_t)v * 16u));
@@ -1137,9 +1138,72 @@ __device__ __forceinline__ void matvec_rows(SharedState &sh, const uint16_t *mat
     }
 }
 
+// The first item of a wave in matvec_rows (rows r0 + 2 * wave and the next),
+// first min(nc, 8) chunks, loaded ahead: issued before a wait on inputs that
+// the weights do not depend on, so the weight stream overlaps the wait.
+constexpr int kAheadChunks = 8;
+struct PairAhead {
+    u32x4 a[kAheadChunks], b[kAheadChunks];
+};
+
+__device__ __forceinline__ void pair_ahead_load(PairAhead &r, const uint16_t *mat, size_t ld, int col0, int nc,
+                                                int r0, int nrows) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (2 * wave >= nrows) return;
+    const int ra = r0 + 2 * wave;
+    const u32x4 *wa = reinterpret_cast<const u32x4 *>(mat + (size_t)ra * ld + col0) + lane;
+    const u32x4 *wb = reinterpret_cast<const u32x4 *>(mat + (size_t)(ra + 1) * ld + col0) + lane;
+#pragma unroll
+    for (int i = 0; i < kAheadChunks; ++i)
+        if (i < nc) {
+            r.a[i] = load_stream(wa + i * 64);
+            r.b[i] = load_stream(wb + i * 64);
+        }
+}
+
+// matvec_rows whose first item per wave was loaded by pair_ahead_load with
+// the same arguments.
+template <typename Fn>
+__device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhead &pre, const uint16_t *mat,
+                                                  size_t ld, int col0, int nc, const u32x4 *x, int r0, int nrows,
+                                                  Fn fn) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (2 * wave < nrows) {
+        const int ra = r0 + 2 * wave;
+        float aa = 0.f, ab = 0.f;
+#pragma unroll
+        for (int i = 0; i < kAheadChunks; ++i)
+            if (i < nc) {
+                aa = dot8(pre.a[i], x[lane + i * 64], aa);
+                ab = dot8(pre.b[i], x[lane + i * 64], ab);
+            }
+        if (nc > kAheadChunks) {
+            const uint16_t *row_a = mat + (size_t)ra * ld + col0 + kAheadChunks * kChunkElems;
+            dot_pair(row_a, row_a + ld, x + kAheadChunks * 64, x + kAheadChunks * 64, nc - kAheadChunks, lane, aa, ab);
+        }
+        aa = wave_sum(aa);
+        ab = wave_sum(ab);
+        if (lane == 0) {
+            fn(ra, aa);
+            fn(ra + 1, ab);
+        }
+    }
+    for (int it = next_local_item(sh, lane); 2 * it < nrows; it = next_local_item(sh, lane)) {
+        const int ra = r0 + 2 * it;
+        float aa = 0.f, ab = 0.f;
+        dot_pair(mat + (size_t)ra * ld + col0, mat + (size_t)(ra + 1) * ld + col0, x, x, nc, lane, aa, ab);
+        aa = wave_sum(aa);
+        ab = wave_sum(ab);
+        if (lane == 0) {
+            fn(ra, aa);
+            fn(ra + 1, ab);
+        }
+    }
+}
+
 // ---- opcode 1: Mixtral_QKV  (python_vm.py:61-118) -------------------------
 
-__device__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                        int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1152,16 +1216,19 @@ __device__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int3
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    const int r0 = b0 * a.qkv_bs, nrows = (b1 - b0) * a.qkv_bs;
+    const uint16_t *wq = a.qkv + (size_t)layer * qkv_rows * p.H;
+    PairAhead pre;
+    pair_ahead_load(pre, wq, (size_t)p.H, 0, p.H / kChunkElems, r0, nrows);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 1, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.attn_ln + (size_t)layer * p.H);
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
-    const int r0 = b0 * a.qkv_bs, nrows = (b1 - b0) * a.qkv_bs;
     float *rowv = reinterpret_cast<float *>(act + (p.H >> 3));  // the block's outputs, bf16-rounded
-    matvec_rows(sh, a.qkv + (size_t)layer * qkv_rows * p.H, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
-                [&](int r, float s) { rowv[r - r0] = rbf(s); });
+    matvec_rows_ahead(sh, pre, wq, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
+                      [&](int r, float s) { rowv[r - r0] = rbf(s); });
     __syncthreads();
 
     // RoPE on q and k rows (interleaved pairs (2i, 2i+1) share cos/sin[2i]):
@@ -1207,20 +1274,86 @@ __device__ __forceinline__ float group_sum(float v, int G) {
     return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Scores are kept in log2 units: q is pre-scaled by attn_scale * log2(e), so
+// that exp(s) = exp2(s2) and a partition's LSE is log2(sum exp2(s2 - M2)) + M2.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void widen8(u32x4 x, float (&f)[8]) {
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf2f(w[j] & 0xffffu);
+        f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+}
+
+// K/V staging for opcode 2: the partition's rows pass through an LDS ring of
+// `kv_ring` chunks.  A chunk holds CT = 8 KiB / (2 D) positions: their K rows
+// (8 KiB), then their V rows (8 KiB).  Wave w stages and reads only its own
+// 1 KiB of each half (positions w * TPW .. + TPW of the chunk), one 16-byte
+// piece (dims dp * 8 .. + 8 of position slot) per lane in lane order, which
+// is the order global_load_lds writes LDS in; so staging and use need no
+// workgroup barrier, only the wave's own wait for its loads.
+constexpr int kKvChunkBytes = 16384;
+constexpr int kKvRingMax = 8;
+constexpr int kAttnSub = 4;  // ring slots scored per softmax rescale
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void global_void_t;
+
+__device__ __forceinline__ void stage_kv(unsigned char *dst, const uint16_t *kbase, const uint16_t *vbase,
+                                         uint32_t row_bytes, int t, int dp) {
+    const size_t off = (size_t)t * row_bytes + (size_t)dp * 16u;
+    __builtin_amdgcn_global_load_lds((global_void_t *)(reinterpret_cast<const char *>(kbase) + off),
+                                     (lds_void_t *)dst, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void_t *)(reinterpret_cast<const char *>(vbase) + off),
+                                     (lds_void_t *)(dst + kKvChunkBytes / 2), 16, 0, 0);
+}
+
+// Split-KV partial attention of query heads kv * GQA .. + GQA over the
+// partition's positions [t0, t1).  Positions before pos_id were written by
+// earlier launches, so the first ring of them is staged before the wait on
+// the QKV counters; the new position's rows (written by this launch) are
+// read after it with device-coherent loads and patched into the ring.
+// Scores are kept in log2 units (q pre-scaled by attn_scale * log2(e)), so
+// exp(s) = exp2(s2) and the partition's LSE is log2(L) + M.
 template <int GQA>
-__device__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState &sh, u32x4 *act, const Ctx &c,
                              int layer, int kv, int nparts, int pidx, int32_t *tim) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int D = a.D, G = D / 8, TPW = 64 / G;
+    const int D = a.D, G = D / 8, TPW = 64 / G, CT = kWaves * TPW;
     const int slot = lane / G, dp = lane % G;
     const int h0 = kv * GQA;
+    const int nb = a.kv_ring;
+    const int pos = (int)p.pos, seq = pos + 1;
+    const int total = (seq + a.kv_bs - 1) / a.kv_bs;
+    const int per = (total + nparts - 1) / nparts;
+    const int tb0 = pidx * per, tb1 = min(tb0 + per, total);
+    const int t0 = tb0 * a.kv_bs, t1 = min(tb1 * a.kv_bs, seq);
+    const int nch = t1 > t0 ? (t1 - t0 + CT - 1) / CT : 0;
+    const int first = t0 + wave * TPW + slot;  // this lane's position in chunk 0
+    const bool has_new = pos >= t0 && pos < t1;
+    const int c_new = has_new ? (pos - t0) / CT : -1;
+    const bool own_new = has_new && ((pos - t0) % CT) / TPW == wave;  // uniform
+
+    unsigned char *ring = reinterpret_cast<unsigned char *>(act);
+    unsigned char *wave_lds = ring + wave * 1024;  // the wave's piece of ring slot 0
+    u32x4 *kl = reinterpret_cast<u32x4 *>(wave_lds) + lane;
+    // K and V of this layer and KV head: position t at byte (t * Hkv * D) * 2
+    const uint16_t *kbase = a.kc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
+    const uint16_t *vbase = a.vc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
+    const uint32_t row_bytes = (uint32_t)(a.Hkv * D * 2);
+    auto stage_round = [&](int r) {
+        for (int k = 0; k < nb; ++k) {
+            const int ch = r * nb + k;
+            if (ch >= nch) break;
+            const int t = first + ch * CT;
+            stage_kv(wave_lds + k * kKvChunkBytes, kbase, vbase, row_bytes, (t < t1 && t != pos) ? t : t0, dp);
+        }
+    };
+    stage_round(0);
 
     // producers: the GQA query heads, the key head and the value head
     const int bph = D / a.qkv_bs;
@@ -1230,85 +1363,121 @@ __device__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState 
     if (!wait_lanes_ge(p, sh, mine, GQA + 2, bph, c, 2, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
-    const int seq = (int)p.pos + 1;
-    const int total = (seq + a.kv_bs - 1) / a.kv_bs;
-    const int per = (total + nparts - 1) / nparts;
-    const int tb0 = pidx * per, tb1 = min(tb0 + per, total);
-    const int t0 = tb0 * a.kv_bs, t1 = min(tb1 * a.kv_bs, seq);
-
+    const float qscale = a.attn_scale * kLog2e;
     float q[GQA][8];
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
-        const u32x4 qv = ld_dev128(a.q_rope, (uint32_t)(((h0 + h) * D + dp * 8) * 2));
-        const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+        widen8(ld_dev128(a.q_rope, (uint32_t)(((h0 + h) * D + dp * 8) * 2)), q[h]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            q[h][2 * j] = bf2f(w[j] & 0xffffu);
-            q[h][2 * j + 1] = bf2f(w[j] >> 16);
-        }
+        for (int j = 0; j < 8; ++j) q[h][j] *= qscale;
     }
-    float m[GQA], l[GQA], acc[GQA][8];
+    float M[GQA], L[GQA], acc[GQA][8];
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.f;
+        M[h] = -INFINITY;
+        L[h] = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
     }
-    // K and V of this layer and KV head: position t at byte (t * Hkv * D) * 2
-    const uint16_t *kbase = a.kc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
-    const uint16_t *vbase = a.vc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
-    const uint32_t row_bytes = (uint32_t)(a.Hkv * D * 2);
-    const int steps = (t1 - t0 + TPW - 1) / TPW;  // <= 0 for an empty partition
-    for (int st = wave; st < steps; st += kWaves) {
-        const int t = t0 + st * TPW + slot;
-        const bool valid = t < t1;
-        const uint32_t off = (uint32_t)(valid ? t : t0) * row_bytes + (uint32_t)dp * 16u;
-        const u32x4 kx = ld_dev128(kbase, off);
-        const u32x4 vx = ld_dev128(vbase, off);
-        const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
-        const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
+    const int rounds = (nch + nb - 1) / nb;
+    for (int r = 0; r < rounds; ++r) {
+        if (r > 0) stage_round(r);
+        // the new position's rows, device-coherent, patched over the row t0
+        // that was staged in their place
+        const bool patch = own_new && c_new / nb == r;  // uniform
+        u32x4 kn = {0u, 0u, 0u, 0u}, vn = {0u, 0u, 0u, 0u};
+        if (patch) {
+            const uint32_t off = (uint32_t)pos * row_bytes + (uint32_t)dp * 16u;
+            kn = ld_dev128(kbase, off);
+            vn = ld_dev128(vbase, off);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging has landed in LDS
+        if (patch && first + c_new * CT == pos) {
+            const int k = c_new - r * nb;
+            kl[k * (kKvChunkBytes / 16)] = kn;
+            kl[k * (kKvChunkBytes / 16) + kKvChunkBytes / 32] = vn;
+        }
+        for (int k0 = 0; k0 < nb; k0 += kAttnSub) {
+            // scores of ring slots k0 .. k0 + kAttnSub
+            float sc[GQA][kAttnSub];
 #pragma unroll
-        for (int h = 0; h < GQA; ++h) {
-            float s = 0.f;
+            for (int u = 0; u < kAttnSub; ++u) {
+                const int k = k0 + u, ch = r * nb + k;
+                const bool live = k < nb && ch < nch;  // uniform
+                const bool valid = live && first + ch * CT < t1;
+                float kf[8];
+                if (live) widen8(kl[k * (kKvChunkBytes / 16)], kf);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s = fmaf(q[h][2 * j], bf2f(kw[j] & 0xffffu), s);
-                s = fmaf(q[h][2 * j + 1], bf2f(kw[j] >> 16), s);
+                for (int h = 0; h < GQA; ++h) {
+                    float d = 0.f;
+                    if (live) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) d = fmaf(q[h][j], kf[j], d);
+                        d = group_sum(d, G);
+                    }
+                    sc[h][u] = valid ? d : -INFINITY;
+                }
             }
-            s = group_sum(s, G) * a.attn_scale;
-            if (!valid) s = -INFINITY;
-            const float mn = fmaxf(m[h], wave_max(s));  // finite: the step has a valid token
-            const float alpha = expf(m[h] - mn);        // 0 while m is -inf
-            const float pr = valid ? expf(s - mn) : 0.f;
-            l[h] = l[h] * alpha + (dp == 0 ? pr : 0.f);
+            // rescale the slot's running state once, to the new max
+            float ref[GQA];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[h][2 * j] = acc[h][2 * j] * alpha + pr * bf2f(vw[j] & 0xffffu);
-                acc[h][2 * j + 1] = acc[h][2 * j + 1] * alpha + pr * bf2f(vw[j] >> 16);
+            for (int h = 0; h < GQA; ++h) {
+                float mb = M[h];
+#pragma unroll
+                for (int u = 0; u < kAttnSub; ++u) mb = fmaxf(mb, sc[h][u]);
+                ref[h] = mb == -INFINITY ? 0.f : mb;
+                const float alpha = exp2_fast(M[h] - ref[h]);  // 0 while M is -inf, 1 if the max holds
+                L[h] *= alpha;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[h][j] *= alpha;
+                M[h] = mb;
             }
-            m[h] = mn;
+#pragma unroll
+            for (int u = 0; u < kAttnSub; ++u) {
+                const int k = k0 + u, ch = r * nb + k;
+                if (!(k < nb && ch < nch)) continue;  // uniform
+                // rows staged for masked positions may hold anything
+                // (the row pos_id is read before this launch writes it)
+                const u32x4 vraw = first + ch * CT < t1 ? kl[k * (kKvChunkBytes / 16) + kKvChunkBytes / 32]
+                                                        : u32x4{0u, 0u, 0u, 0u};
+                float vf[8];
+                widen8(vraw, vf);
+#pragma unroll
+                for (int h = 0; h < GQA; ++h) {
+                    const float pr = exp2_fast(sc[h][u] - ref[h]);  // 0 for masked positions
+                    L[h] += pr;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pr, vf[j], acc[h][j]);
+                }
+            }
         }
     }
-    // fold the token slots of the wave together (lanes with the same dp);
-    // l is carried by the dp == 0 lane of each slot, so a wave sum totals it
+
+    // fold the token slots of the wave (lanes with the same dp) to the wave max
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
+        float mw = M[h];
+        for (int o = G; o < 64; o <<= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
+        const float f = M[h] == -INFINITY ? 0.f : exp2_fast(M[h] - mw);
+        L[h] *= f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] *= f;
         for (int o = G; o < 64; o <<= 1) {
+            L[h] += __shfl_xor(L[h], o);
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[h][j] += __shfl_xor(acc[h][j], o);
         }
-        l[h] = wave_sum(l[h]);
+        M[h] = mw;
     }
-    // per-wave partials to LDS: m, l [kWaves][GQA], acc [kWaves][GQA][D]
-    float *wm = reinterpret_cast<float *>(act);
+    // per-wave partials to LDS after the ring: m, l [kWaves][GQA], acc [kWaves][GQA][D]
+    float *wm = reinterpret_cast<float *>(ring + (size_t)nb * kKvChunkBytes);
     float *wl = wm + kWaves * GQA;
     float *wacc = wl + kWaves * GQA;
     if (lane == 0) {
 #pragma unroll
         for (int h = 0; h < GQA; ++h) {
-            wm[wave * GQA + h] = m[h];
-            wl[wave * GQA + h] = l[h];
+            wm[wave * GQA + h] = M[h];
+            wl[wave * GQA + h] = L[h];
         }
     }
     if (slot == 0) {
@@ -1320,25 +1489,25 @@ __device__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState 
     __syncthreads();
     for (int i = threadIdx.x; i < GQA * D; i += kThreads) {
         const int h = i / D, d = i % D;
-        float M = -INFINITY;
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w * GQA + h]);
-        float L = 0.f, O = 0.f;
-        if (M != -INFINITY) {
+        float Mx = -INFINITY;
+        for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, wm[w * GQA + h]);
+        float Ls = 0.f, O = 0.f;
+        if (Mx != -INFINITY) {
             for (int w = 0; w < kWaves; ++w) {
                 const float mw = wm[w * GQA + h];
                 if (mw == -INFINITY) continue;
-                const float f = expf(mw - M);
-                L += wl[w * GQA + h] * f;
+                const float f = exp2_fast(mw - Mx);
+                Ls += wl[w * GQA + h] * f;
                 O += wacc[(w * GQA + h) * D + d] * f;
             }
         }
-        const float out = L > 0.f ? O / L : 0.f;
+        const float out = Ls > 0.f ? O / Ls : 0.f;
         if (a.skip_red) {
             st_dev16(a.attn_out + (h0 + h) * D + d, f2bf(out));
         } else {
             st_dev32(a.out_int + ((size_t)(h0 + h) * a.P + pidx) * D + d, __float_as_uint(out));
             if (d == 0) {
-                const float lse = L > 0.f ? log2f(L) + M * kLog2e : -INFINITY;
+                const float lse = Ls > 0.f ? log2f(Ls) + Mx : -INFINITY;
                 st_dev32(a.lse_int + (size_t)(h0 + h) * a.P + pidx, __float_as_uint(lse));
             }
         }
@@ -1352,7 +1521,7 @@ __device__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState 
     return true;
 }
 
-__device__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                                 int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int kv = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1374,7 +1543,7 @@ __device__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, c
 
 // ---- opcode 3: Mixtral_AttnReduction  (python_vm.py:166-189) --------------
 
-__device__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32_t *ins, const Ctx &c,
                                   int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int hs = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1399,23 +1568,45 @@ __device__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32
     if (!wait_ge(p, sh, bar_at(p, layer, 2) + hs, nparts, c, 3, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     const int D = a.D;
+    // weights 2^(lse_k - max lse) and their sum: wave h, lane k (all n loads
+    // in flight at once)
+    static_assert(kRowBatchLds * 2 * kMaxSegments >= 4 * 64 + 4 + 64, "reduction staging fits in sh.part");
+    float *wts = reinterpret_cast<float *>(sh.part);  // [gqa][64]
+    float *den = wts + 4 * 64;                        // [gqa]
+    int *slots = reinterpret_cast<int *>(den + 4);    // [n]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave < gqa) {
+        const int s = lane < n ? ins[6 + lane] : 0;
+        float lse = lane < n ? __uint_as_float(ld_dev32(a.lse_int + (size_t)(hs + wave) * a.P + s)) : -INFINITY;
+        float mx = lse;
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float f = lane < n ? exp2f(lse - mx) : 0.f;
+        const float tot = wave_sum(f);
+        wts[wave * 64 + lane] = f;
+        if (lane == 0) den[wave] = tot;
+        if (wave == 0 && lane < n) slots[lane] = s;
+    }
+    __syncthreads();
     for (int i = threadIdx.x; i < gqa * D; i += kThreads) {
-        const int h = hs + i / D, d = i % D;
-        float M = -INFINITY;
-        for (int k = 0; k < n; ++k) M = fmaxf(M, __uint_as_float(ld_dev32(a.lse_int + (size_t)h * a.P + ins[6 + k])));
-        float den = 0.f, num = 0.f;
-        for (int k = 0; k < n; ++k) {
-            const int s = ins[6 + k];
-            const float f = exp2f(__uint_as_float(ld_dev32(a.lse_int + (size_t)h * a.P + s)) - M);
-            den += f;
-            num += __uint_as_float(ld_dev32(a.out_int + ((size_t)h * a.P + s) * D + d)) * f;
+        const int hl = i / D, h = hs + hl, d = i % D;
+        const float *out = a.out_int + (size_t)h * a.P * D + d;
+        const float *f = wts + hl * 64;
+        float num = 0.f;
+        int k = 0;
+        for (; k + 8 <= n; k += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = __uint_as_float(ld_dev32(out + (size_t)slots[k + u] * D));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) num = fmaf(v[u], f[k + u], num);
         }
-        const float red = num / den;
+        for (; k < n; ++k) num = fmaf(__uint_as_float(ld_dev32(out + (size_t)slots[k] * D)), f[k], num);
+        const float red = num / den[hl];
         if (terminal) {
             st_dev16(a.attn_out + h * D + d, f2bf(red));
         } else {
             st_dev32(a.out_int + ((size_t)h * a.P + out_slot) * D + d, __float_as_uint(red));
-            if (d == 0) st_dev32(a.lse_int + (size_t)h * a.P + out_slot, __float_as_uint(logf(den)));
+            if (d == 0) st_dev32(a.lse_int + (size_t)h * a.P + out_slot, __float_as_uint(logf(den[hl])));
         }
     }
     drain_and_sync();
@@ -1426,7 +1617,7 @@ __device__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32
 
 // ---- opcode 4: Mixtral_OProj  (python_vm.py:196-215) ----------------------
 
-__device__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                          int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1439,18 +1630,21 @@ __device__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const in
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    const int K = a.Hq * a.D;  // reduction length
+    const uint16_t *wo = a.oproj + (size_t)layer * p.H * K;
+    PairAhead pre;
+    pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, b0 * p.oproj_bs, (b1 - b0) * p.oproj_bs);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    const int K = a.Hq * a.D;  // reduction length
     for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(a.attn_out, (uint32_t)v * 16u);
     __syncthreads();
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    matvec_rows(sh, a.oproj + (size_t)layer * p.H * K, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs,
-                (b1 - b0) * p.oproj_bs, [&](int r, float s) {
-                    uint16_t *hp = p.hidden + r;
-                    st_dev16(hp, f2bf(bf2f(ld_dev16(hp)) + rbf(s)));
-                });
+    matvec_rows_ahead(sh, pre, wo, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs, (b1 - b0) * p.oproj_bs,
+                      [&](int r, float s) {
+                          uint16_t *hp = p.hidden + r;
+                          st_dev16(hp, f2bf(bf2f(ld_dev16(hp)) + rbf(s)));
+                      });
     drain_and_sync();
     arrive(bar_at(p, layer, 4), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
@@ -1461,7 +1655,7 @@ __device__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const in
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-__device__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1636,23 +1830,33 @@ struct DeviceGuard {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-size_t lds_bytes_for(const mk_mixtral_globals *g) {
+// Dynamic LDS for the launch with an opcode-2 ring of `kv_ring` chunks
+// (ignored without attention tensors).
+size_t lds_bytes_for(const mk_mixtral_globals *g, int kv_ring) {
     const size_t normed = (size_t)g->hidden_size * 2;
     // both SiLU rows, then the opcode-6 cache-warming sink (1 KiB per wave)
     const size_t silu = (size_t)g->intermediate_size * 2 * 2 + (size_t)kWaves * 1024;
     size_t need = normed > silu ? normed : silu;
     if (g->qkv_weights != nullptr) {
         const size_t Hq = (size_t)g->num_attention_heads, Hkv = (size_t)g->num_kv_heads, D = (size_t)g->head_dim;
-        // opcode 1: normed hidden + one fp32 per QKV row; opcode 2: per-wave
-        // softmax partials; opcode 4: attn_out
+        // opcode 1: normed hidden + one fp32 per QKV row; opcode 2: the K/V
+        // ring, then per-wave softmax partials; opcode 4: attn_out
         const size_t qkv = normed + (Hq + 2 * Hkv) * D * 4;
-        const size_t attn = (size_t)kWaves * (Hq / Hkv) * (D + 2) * 4;
+        const size_t attn = (size_t)kv_ring * kKvChunkBytes + (size_t)kWaves * (Hq / Hkv) * (D + 2) * 4;
         const size_t oproj = Hq * D * 2;
         need = need > qkv ? need : qkv;
         need = need > attn ? need : attn;
         need = need > oproj ? need : oproj;
     }
     return need > (size_t)kMinLdsBytes ? need : (size_t)kMinLdsBytes;
+}
+
+// Largest opcode-2 ring (chunks, <= kKvRingMax) whose launch fits in
+// `max_lds` bytes of LDS per workgroup; 0 if even one chunk does not.
+int kv_ring_for(const mk_mixtral_globals *g, size_t max_lds) {
+    for (int nb = kKvRingMax; nb >= 1; --nb)
+        if (lds_bytes_for(g, nb) + sizeof(SharedState) <= max_lds) return nb;
+    return 0;
 }
 
 // The attention tensors are optional (an MoE-only launch passes none); when
@@ -1766,8 +1970,9 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     rc = device_state(dev, &st);
     if (rc != MK_OK) return rc;
 
-    const size_t lds = lds_bytes_for(g);
-    if (lds + sizeof(SharedState) > (size_t)st->max_lds) return MK_ERR_UNSUPPORTED;
+    const int kv_ring = kv_ring_for(g, (size_t)st->max_lds);
+    if (kv_ring < 1) return MK_ERR_UNSUPPORTED;
+    const size_t lds = lds_bytes_for(g, kv_ring);
     int blocks = 0;
     // Mixtral's 8 experts get a kernel specialised for exactly 8
     const bool e8 = g->num_experts == 8;
@@ -1865,6 +2070,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
         a.lm_red = g->lm_head_reduction;
         a.attn_scale = g->attn_scale;
         a.skip_red = g->skip_attn_reduction ? 1 : 0;
+        a.kv_ring = kv_ring;
         if (st->attn == nullptr) {
             std::lock_guard<std::mutex> lock(g_mutex);
             if (st->attn == nullptr &&
