@@ -1219,12 +1219,12 @@ __device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 
     const int r0 = b0 * a.qkv_bs, nrows = (b1 - b0) * a.qkv_bs;
     const uint16_t *wq = a.qkv + (size_t)layer * qkv_rows * p.H;
     PairAhead pre;
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
     pair_ahead_load(pre, wq, (size_t)p.H, 0, p.H / kChunkElems, r0, nrows);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 1, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.attn_ln + (size_t)layer * p.H);
-    stamp(tim, MK_TEVENT_FIRST_LOAD);
 
     float *rowv = reinterpret_cast<float *>(act + (p.H >> 3));  // the block's outputs, bf16-rounded
     matvec_rows_ahead(sh, pre, wq, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
@@ -1353,6 +1353,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
             stage_kv(wave_lds + k * kKvChunkBytes, kbase, vbase, row_bytes, (t < t1 && t != pos) ? t : t0, dp);
         }
     };
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
     stage_round(0);
 
     // producers: the GQA query heads, the key head and the value head
@@ -1633,13 +1634,13 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     const int K = a.Hq * a.D;  // reduction length
     const uint16_t *wo = a.oproj + (size_t)layer * p.H * K;
     PairAhead pre;
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
     pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, b0 * p.oproj_bs, (b1 - b0) * p.oproj_bs);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(a.attn_out, (uint32_t)v * 16u);
     __syncthreads();
-    stamp(tim, MK_TEVENT_FIRST_LOAD);
     matvec_rows_ahead(sh, pre, wo, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs, (b1 - b0) * p.oproj_bs,
                       [&](int r, float s) {
                           uint16_t *hp = p.hidden + r;

@@ -66,6 +66,10 @@ class TimingRecord:
     o_proj_block_size: int = 0
     lm_head_block_size: int = 0
     attn_width: int = 0  # Hq * head_dim, the O-projection's reduction length
+    head_dim: int = 0
+    num_kv_heads: int = 0
+    attn_kv_block_size: int = 0
+    pos_id: int = 0
 
     @classmethod
     def from_globals(cls, globs) -> "TimingRecord":
@@ -82,6 +86,10 @@ class TimingRecord:
             o_proj_block_size=globs.o_proj_block_size,
             lm_head_block_size=globs.lm_head_block_size,
             attn_width=globs.num_attention_heads * globs.head_dim,
+            head_dim=globs.head_dim,
+            num_kv_heads=globs.num_kv_heads,
+            attn_kv_block_size=globs.attn_kv_block_size,
+            pos_id=int(globs.pos_id),
         )
 
     def micros(self) -> np.ndarray:
@@ -120,6 +128,16 @@ class TimingRecord:
             return E * H * 2 + H * 2
         if op == 1 and self.qkv_block_size:
             return (int(ins[3]) - int(ins[2])) * self.qkv_block_size * H * 2
+        if op == 2 and self.head_dim and self.attn_kv_block_size:
+            # K and V rows of the partition's positions (python_vm.py:125-159
+            # split: blocks of attn_kv_block_size over num_partials)
+            nparts, pidx = int(ins[3]), int(ins[4])
+            seq = self.pos_id + 1
+            total = -(-seq // self.attn_kv_block_size)
+            per = -(-total // nparts)
+            t0 = min(pidx * per, total) * self.attn_kv_block_size
+            t1 = min(min(pidx * per + per, total) * self.attn_kv_block_size, seq)
+            return max(t1 - t0, 0) * 2 * self.head_dim * 2
         if op == 4 and self.o_proj_block_size:
             return (int(ins[3]) - int(ins[2])) * self.o_proj_block_size * self.attn_width * 2
         if op == 7 and self.lm_head_block_size:
@@ -132,14 +150,14 @@ def save_record(path, rec: TimingRecord) -> None:
         path, timings=rec.timings, instructions=rec.instructions,
         shape=np.array([rec.hidden_size, rec.intermediate_size, rec.num_experts,
                         rec.expert_proj_block_size, rec.down_proj_block_size, rec.k,
-                        rec.qkv_block_size, rec.o_proj_block_size, rec.lm_head_block_size, rec.attn_width]))
+                        rec.qkv_block_size, rec.o_proj_block_size, rec.lm_head_block_size, rec.attn_width,
+                        rec.head_dim, rec.num_kv_heads, rec.attn_kv_block_size, rec.pos_id]))
 
 
 def load_record(path) -> TimingRecord:
     d = np.load(Path(path), allow_pickle=False)
-    shape = [int(x) for x in d["shape"]] + [0] * 4
-    H, F, E, ebs, dbs, k, qbs, obs, lbs, aw = shape[:10]
-    return TimingRecord(d["timings"], d["instructions"], H, F, E, ebs, dbs, k, qbs, obs, lbs, aw)
+    shape = [int(x) for x in d["shape"]] + [0] * 8
+    return TimingRecord(d["timings"], d["instructions"], *shape[:14])
 
 
 def barrier_waits(rec: TimingRecord) -> dict:

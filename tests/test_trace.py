@@ -84,3 +84,31 @@ def test_phase_summary_and_report(tmp_path):
     assert np.array_equal(back.timings, rec.timings) and back.down_proj_block_size == 16
     text = format_report(back)
     assert "RmsRouterUpgate" in text and "streamed" in text
+
+
+@pytest.mark.parametrize("pos,nparts,kvbs", [(0, 1, 16), (4096, 17, 16), (300, 7, 16), (33, 8, 4)])
+def test_partial_attention_bytes_cover_the_cache(pos, nparts, kvbs):
+    """Opcode-2 byte model: the partitions of one KV head read every cached
+    position once, K and V rows of head_dim bf16 each -- the same split as
+    the oracle's partial_token_range."""
+    from oracle import python_vm as oracle
+
+    D = 128
+    ins = np.zeros((1, nparts, 32), dtype=np.int32)
+    for q in range(nparts):
+        ins[0, q, :5] = [2, 0, 3, nparts, q]
+    rec = TimingRecord(np.zeros((1, nparts, 128), np.int32), ins, H, F, E, 8, 16, head_dim=D, num_kv_heads=8,
+                       attn_kv_block_size=kvbs, pos_id=pos)
+    per = [rec.streamed_bytes(0, q) for q in range(nparts)]
+    assert sum(per) == (pos + 1) * 2 * D * 2
+    for q in range(nparts):
+        a, b = oracle.partial_token_range(pos + 1, kvbs, nparts, q)
+        assert per[q] == max(b - a, 0) * 2 * D * 2  # trailing partitions may be empty
+
+
+def test_record_roundtrip_keeps_attention_fields(tmp_path):
+    rec = _record()
+    rec.head_dim, rec.num_kv_heads, rec.attn_kv_block_size, rec.pos_id = 128, 8, 16, 4096
+    save_record(tmp_path / "r.npz", rec)
+    back = load_record(tmp_path / "r.npz")
+    assert (back.head_dim, back.num_kv_heads, back.attn_kv_block_size, back.pos_id) == (128, 8, 16, 4096)
