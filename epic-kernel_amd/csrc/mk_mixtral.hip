@@ -43,6 +43,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "mk_llama.h"
 #include "mk_mixtral.h"
 
 #ifndef MK_THREADS
@@ -134,6 +135,10 @@ struct KParams {
     int32_t attn;
     const struct AttnParams *ap;
     uint32_t pos;  // pos_id: changes every decode step, so it stays a kernel argument
+    // arrivals on [l][5][0] that complete a layer's down-projection (Mixtral:
+    // 2 * H / down_bs; dense Llama: (F / red_cols) * (H / down_bs))
+    int32_t down_arrivals;
+    int32_t red_cols;  // dense down-projection column chunk (matvec_reduction_size)
 };
 
 struct AttnParams {
@@ -1040,7 +1045,7 @@ __device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u3
     router_prefetch<kE>(p, sh, layer, weights, rr);
     if (layer > 0) {
         stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-        if (!wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 8, layer)) return false;
+        if (!wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 8, layer)) return false;
         stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     }
     float logits[Experts<kE>::kMax];
@@ -1222,7 +1227,7 @@ __device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     pair_ahead_load(pre, wq, (size_t)p.H, 0, p.H / kChunkElems, r0, nrows);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), 2 * (p.H / p.down_bs), c, 1, layer)) return false;
+    if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 1, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.attn_ln + (size_t)layer * p.H);
 
@@ -1538,6 +1543,7 @@ __device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &s
     switch (a.Hq / a.Hkv) {
     case 1: return partial_attn<1>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
     case 2: return partial_attn<2>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
+    case 3: return partial_attn<3>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
     default: return partial_attn<4>(p, a, sh, act, c, layer, kv, nparts, pidx, tim);
     }
 }
@@ -1670,7 +1676,7 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, last, 6), 2 * (p.H / p.down_bs), c, 7, last)) return false;
+    if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.lm_norm);
     stamp(tim, MK_TEVENT_FIRST_LOAD);
@@ -1705,6 +1711,152 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
 // keeps the register allocation of the opcode 5/6 streaming loops free of
 // the attention code's live ranges; launches without attention tensors use
 // it.
+// ---------------------------------------------------------------------------
+// dense (Llama) opcodes 5-7  (lat/python_vm.py:83-196)
+// ---------------------------------------------------------------------------
+
+// Opcode 5, LayerNormDoubleMatVecSiLU [5, layer, n, block...]: RMSNorm with
+// the MLP norm, then for each listed block of up_gate_proj_block_size rows
+// silu_out[r] = bf16(bf16(silu(bf16 g)) * bf16 u), g and u the gate and up
+// rows dotted with the normed vector; one arrival per block on [l][4][0].
+// The dense weights are the one-expert case of the opcode-5 item.
+__device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+                                                const Ctx &c, int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int n = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int nblocks = p.F / p.expert_bs;
+    bool bad = layer < 0 || layer >= p.num_layers || n < 0 || n > MK_INTS_PER_INSTRUCTION - 3;
+    for (int i = 0; !bad && i < n; ++i) {
+        const int b = __builtin_amdgcn_readfirstlane(ins[3 + i]);
+        bad = b < 0 || b >= nblocks;
+    }
+    if (bad) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 5, layer, n, nblocks);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    rms_to_lds(p, sh, act, p.ffn_ln + (size_t)layer * p.H);
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int items = n * p.expert_bs;
+    for (int it = wave; it < items; it = next_local_item(sh, lane)) {
+        const int k = it / p.expert_bs;
+        const int b = __builtin_amdgcn_readfirstlane(ins[3 + k]);
+        upgate_item(p, act, layer, b * p.expert_bs, p.expert_bs, 0, 0, it - k * p.expert_bs, lane);
+    }
+    drain_and_sync();
+    arrive(bar_at(p, layer, 5), n);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// Opcode 6, DownProjResidual [6, layer, start, end, red]: rows
+// [start, end) * down_proj_block_size of the down projection, columns
+// [red, red + 1) * red_cols, dotted with those columns of silu_out; each row
+// pair is added into hidden with one packed bf16 atomic (the column chunks
+// of a row run on different workgroups), h = bf16(h + bf16(partial)).
+// Arrival end - start on [l][5][0].
+__device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+                                              const Ctx &c, int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
+    const int red = __builtin_amdgcn_readfirstlane(ins[4]);
+    const int R = p.red_cols;
+    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.down_bs > p.H || red < 0 ||
+        (int64_t)(red + 1) * R > p.F) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 6, layer, b0, red);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    const int col0 = red * R;
+    for (int v = threadIdx.x; v < (R >> 3); v += kThreads)
+        act[v] = ld_dev128(p.silu, (uint32_t)(col0 + v * 8) * 2u);
+    __syncthreads();
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = b0 * p.down_bs, nrows = (b1 - b0) * p.down_bs;
+    const uint16_t *w = p.down + (size_t)layer * p.H * p.F;
+    for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
+        const int ra = r0 + 2 * it;
+        float aa = 0.f, ab = 0.f;
+        dot_pair(w + (size_t)ra * p.F + col0, w + (size_t)(ra + 1) * p.F + col0, act, act, R / kChunkElems, lane,
+                 aa, ab);
+        aa = wave_sum(aa);
+        ab = wave_sum(ab);
+        if (lane == 0) {
+            const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(aa)),
+                                __builtin_bit_cast(__bf16, (uint16_t)f2bf(ab))};
+            __builtin_amdgcn_global_atomic_fadd_v2bf16((__attribute__((address_space(1))) bf16x2_t *)(p.hidden + ra),
+                                                       v);
+        }
+    }
+    drain_and_sync();
+    arrive(bar_at(p, layer, 6), b1 - b0);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// Opcode 7, RMS_LM_Head [7, start, end]: RMSNorm with the LM-head norm, then
+// logits[r] = bf16(W[r] . normed) over all hidden columns for rows
+// [start, end) * lm_head_block_size (stored, not accumulated).
+__device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+                                                 const Ctx &c, int32_t *tim) {
+    const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int last = p.num_layers - 1;
+    if (!need_attention(p, c, 7, last)) return false;
+    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    if (b0 < 0 || b1 < b0 || (int64_t)b1 * a.lm_bs > a.V) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 7, last, b0, b1);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    rms_to_lds(p, sh, act, a.lm_norm);
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = b0 * a.lm_bs, nrows = (b1 - b0) * a.lm_bs;
+    for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
+        const int ra = r0 + 2 * it;
+        float aa = 0.f, ab = 0.f;
+        dot_pair(a.lm_head + (size_t)ra * p.H, a.lm_head + (size_t)(ra + 1) * p.H, act, act, p.H / kChunkElems, lane,
+                 aa, ab);
+        aa = wave_sum(aa);
+        ab = wave_sum(ab);
+        if (lane == 0) st_dev32(a.logits + ra, f2bf(aa) | (f2bf(ab) << 16));
+    }
+    drain_and_sync();
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// Exit protocol: the last workgroup out (failed or not) zeroes the
+// work-sharing counters for the next launch.  Every other workgroup has
+// finished all of its scratch accesses before it increments the counter.
+__device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
+    drain_and_sync();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(p.scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.flag = prev == (int)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (sh.flag) {
+        const int n = 2 * (int)gridDim.x * p.queue_len;
+        for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
+        drain_and_sync();
+        if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 template <int kE, bool kAttn>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     extern __shared__ u32x4 act[];
@@ -1750,21 +1902,45 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         if (!ok) break;
     }
 
-    // Exit protocol: the last workgroup out (failed or not) zeroes the
-    // work-sharing counters for the next launch.  Every other workgroup has
-    // finished all of its scratch accesses before it increments the counter.
-    drain_and_sync();
-    if (threadIdx.x == 0) {
-        const int prev = __hip_atomic_fetch_add(p.scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh.flag = prev == (int)gridDim.x - 1;
-    }
+    kernel_exit(p, sh);
+}
+
+// Persistent kernel of the dense Llama VM (lat/ opcodes 1-7): the attention
+// side is shared with the Mixtral kernel; opcodes 5-7 are the dense MLP and
+// the LM head.
+__global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
+    extern __shared__ u32x4 act[];
+    __shared__ SharedState sh;
+    if (threadIdx.x == 0) sh.route_layer = -1;
     __syncthreads();
-    if (sh.flag) {
-        const int n = 2 * (int)gridDim.x * p.queue_len;
-        for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
-        drain_and_sync();
-        if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    const int w = blockIdx.x;
+    for (int q = 0; q < p.queue_len; ++q) {
+        const size_t slot = (size_t)w * p.queue_len + q;
+        const int32_t *ins = p.instructions + slot * MK_INTS_PER_INSTRUCTION;
+        int32_t *tim = p.timings != nullptr ? p.timings + slot * MK_TIMING_SLOTS : nullptr;
+        const int op = __builtin_amdgcn_readfirstlane(ins[0]);
+        const Ctx c{w, q};
+        stamp(tim, MK_TEVENT_START);
+        bool ok = true;
+        switch (op) {
+        case 0: break;
+        case 1: ok = op_qkv(p, sh, act, ins, c, tim); break;
+        case 2: ok = op_partial_attn(p, sh, act, ins, c, tim); break;
+        case 3: ok = op_attn_reduction(p, sh, ins, c, tim); break;
+        case 4: ok = op_oproj(p, sh, act, ins, c, tim); break;
+        case 5: ok = op_dense_upgate(p, sh, act, ins, c, tim); break;
+        case 6: ok = op_dense_down(p, sh, act, ins, c, tim); break;
+        case 7: ok = op_dense_lm_head(p, sh, act, ins, c, tim); break;
+        default:
+            report_error(p, MK_ERR_BAD_OPCODE, c, op, 0, 0, op);
+            ok = false;
+            break;
+        }
+        stamp(tim, MK_TEVENT_END);
+        if (!ok) break;
     }
+    kernel_exit(p, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -1830,6 +2006,71 @@ struct DeviceGuard {
 };
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The per-device scratch buffer holds at least `need` ints (exit counter and
+// work-sharing cursors per instruction slot).
+int ensure_scratch(DeviceState *st, size_t need) {
+    if (need <= st->scratch_ints) return MK_OK;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (need <= st->scratch_ints) return MK_OK;
+    hipError_t e;
+    size_t cap = st->scratch_ints ? st->scratch_ints : 4096;
+    while (cap < need) cap *= 2;
+    if (st->scratch != nullptr) {
+        // kernels queued earlier may still use the old buffer
+        if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+        if ((e = hipFree(st->scratch)) != hipSuccess) return hip_fail(e, "hipFree");
+        st->scratch = nullptr;
+        st->scratch_ints = 0;
+    }
+    if ((e = hipMalloc(reinterpret_cast<void **>(&st->scratch), cap * sizeof(int32_t))) != hipSuccess)
+        return hip_fail(e, "hipMalloc");
+    if ((e = hipMemset(st->scratch, 0, cap * sizeof(int32_t))) != hipSuccess) return hip_fail(e, "hipMemset");
+    st->scratch_ints = cap;
+    return MK_OK;
+}
+
+// The device copy of the attention parameters, refreshed only when they
+// change (a decode loop launches the same tensors every step); the copy is
+// stream-ordered after the launches that read the previous contents.
+int upload_attn(DeviceState *st, const AttnParams &a, hipStream_t stream, const AttnParams **out) {
+    hipError_t e;
+    if (st->attn == nullptr) {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (st->attn == nullptr &&
+            (e = hipMalloc(reinterpret_cast<void **>(&st->attn), sizeof(AttnParams))) != hipSuccess)
+            return hip_fail(e, "hipMalloc");
+    }
+    if (std::memcmp(&a, &st->attn_host, sizeof(a)) != 0) {
+        if ((e = hipMemcpyAsync(st->attn, &a, sizeof(a), hipMemcpyHostToDevice, stream)) != hipSuccess)
+            return hip_fail(e, "hipMemcpyAsync");
+        st->attn_host = a;
+    }
+    *out = st->attn;
+    return MK_OK;
+}
+
+// Co-residency check, then the launch of `fn` (a persistent kernel over
+// `workers` workgroups).
+int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t lds, KParams &kp,
+                      hipStream_t stream) {
+    int blocks = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds);
+    if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
+    void *args[] = {&kp};
+    e = hipLaunchKernel(fn, dim3((unsigned)workers), dim3(kThreads), args, lds, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel");
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "hipGetLastError");
+    return MK_OK;
+}
+
+uint32_t timeout_ticks(uint32_t spin_timeout_us) {
+    const uint64_t us = spin_timeout_us ? spin_timeout_us : 2000000u;
+    const uint64_t ticks = us * kTicksPerUs;
+    return ticks > 0xffffffffu ? 0xffffffffu : (uint32_t)ticks;
+}
 
 // Dynamic LDS for the launch with an opcode-2 ring of `kv_ring` chunks
 // (ignored without attention tensors).
@@ -1921,9 +2162,153 @@ int validate(const mk_mixtral_globals *g) {
     return validate_attention(g);
 }
 
+// ---- dense Llama launches ----
+
+size_t lds_bytes_llama(const mk_llama_globals *g, int kv_ring) {
+    const size_t H = (size_t)g->hidden_size, Hq = (size_t)g->num_attention_heads,
+                 Hkv = (size_t)g->num_kv_heads, D = (size_t)g->head_dim;
+    size_t need = H * 2;                                         // normed hidden (opcodes 5, 7)
+    const size_t qkv = H * 2 + (Hq + 2 * Hkv) * D * 4;           // opcode 1
+    const size_t attn = (size_t)kv_ring * kKvChunkBytes + (size_t)kWaves * (Hq / Hkv) * (D + 2) * 4;  // opcode 2
+    const size_t oproj = Hq * D * 2;                             // opcode 4
+    const size_t down = (size_t)g->matvec_reduction_size * 2;    // opcode 6
+    for (size_t v : {qkv, attn, oproj, down}) need = need > v ? need : v;
+    return need > (size_t)kMinLdsBytes ? need : (size_t)kMinLdsBytes;
+}
+
+int kv_ring_llama(const mk_llama_globals *g, size_t max_lds) {
+    for (int nb = kKvRingMax; nb >= 1; --nb)
+        if (lds_bytes_llama(g, nb) + sizeof(SharedState) <= max_lds) return nb;
+    return 0;
+}
+
+int validate_llama(const mk_llama_globals *g) {
+    if (g == nullptr || g->struct_size < sizeof(mk_llama_globals) || g->abi_version != MK_LLAMA_ABI_VERSION)
+        return MK_ERR_INVALID_ARGUMENT;
+    if (!g->barriers || !g->instructions || !g->qkv_weights || !g->attn_norm_weights || !g->o_weights ||
+        !g->mlp_norm_weights || !g->up_weights || !g->gate_weights || !g->down_weights ||
+        !g->lm_head_norm_weights || !g->lm_head_weights || !g->k_cache || !g->v_cache || !g->rope_cos ||
+        !g->rope_sin || !g->hidden_states || !g->q_post_rope || !g->attn_out || !g->attn_lse_intermediates ||
+        !g->attn_out_intermediates || !g->silu_out || !g->logits)
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->num_workers < 1 || g->queue_len < 1 || g->num_workers > (1 << 20) || g->queue_len > (1 << 20))
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->num_layers < 1 || g->bar_layers < g->num_layers || g->bar_ops < 7 || g->bar_width < 1)
+        return MK_ERR_INVALID_ARGUMENT;
+    const int H = g->hidden_size, F = g->intermediate_size, Hq = g->num_attention_heads, Hkv = g->num_kv_heads,
+              D = g->head_dim;
+    if (H < kChunkElems || H % kChunkElems || F < 2 || (int64_t)F * H > (INT64_C(1) << 40)) return MK_ERR_UNSUPPORTED;
+    if (Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 4) return MK_ERR_UNSUPPORTED;
+    if (D != 64 && D != 128) return MK_ERR_UNSUPPORTED;
+    if ((Hq * D) % kChunkElems) return MK_ERR_UNSUPPORTED;
+    if (g->bar_width < Hq + 2 * Hkv) return MK_ERR_INVALID_ARGUMENT;
+    const int R = g->matvec_reduction_size;
+    if (R < kChunkElems || R % kChunkElems || F % R) return MK_ERR_UNSUPPORTED;
+    if (g->up_gate_proj_block_size < 1 || F % g->up_gate_proj_block_size || g->down_proj_block_size < 2 ||
+        g->down_proj_block_size % 2 || H % g->down_proj_block_size || g->o_proj_block_size < 2 ||
+        g->o_proj_block_size % 2 || H % g->o_proj_block_size)
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->qkv_block_size < 2 || g->qkv_block_size % 2 || D % g->qkv_block_size) return MK_ERR_INVALID_ARGUMENT;
+    if (g->lm_head_block_size < 2 || g->lm_head_block_size % 2 || g->vocab_size < 1 ||
+        g->vocab_size % g->lm_head_block_size || g->attn_kv_block_size < 1)
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->kv_capacity < 1 || (int64_t)g->pos_id >= g->kv_capacity || g->attn_partial_slots < 1)
+        return MK_ERR_INVALID_ARGUMENT;
+    if ((int64_t)g->kv_capacity * Hkv * D * 2 > (INT64_C(1) << 31) - 1) return MK_ERR_UNSUPPORTED;
+    if (!(g->rms_norm_eps >= 0.0f) || !isfinite(g->rms_norm_eps)) return MK_ERR_INVALID_ARGUMENT;
+    const void *vec[] = {g->qkv_weights, g->attn_norm_weights, g->o_weights, g->mlp_norm_weights, g->up_weights,
+                         g->gate_weights, g->down_weights, g->lm_head_norm_weights, g->lm_head_weights, g->k_cache,
+                         g->v_cache, g->hidden_states, g->q_post_rope, g->attn_out, g->silu_out};
+    for (const void *v : vec)
+        if (!aligned16(v)) return MK_ERR_INVALID_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(g->logits) & 3u) return MK_ERR_INVALID_ARGUMENT;
+    return MK_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int mk_llama_abi_version(void) { return MK_LLAMA_ABI_VERSION; }
+
+int mk_llama_launch(const mk_llama_globals *g, void *stream) {
+    int rc = validate_llama(g);
+    if (rc != MK_OK) return rc;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    DeviceState *st = nullptr;
+    rc = device_state(dev, &st);
+    if (rc != MK_OK) return rc;
+    const int kv_ring = kv_ring_llama(g, (size_t)st->max_lds);
+    if (kv_ring < 1) return MK_ERR_UNSUPPORTED;
+    const size_t lds = lds_bytes_llama(g, kv_ring);
+    rc = ensure_scratch(st, kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len);
+    if (rc != MK_OK) return rc;
+
+    KParams kp{};
+    kp.instructions = g->instructions;
+    kp.timings = g->record_timings ? g->timings : nullptr;
+    kp.bar = g->barriers;
+    kp.status = g->status != nullptr ? g->status : st->status;
+    // the dense MLP is the one-expert case of the MoE weight layout
+    kp.gate = g->gate_weights;
+    kp.up = g->up_weights;
+    kp.down = g->down_weights;
+    kp.ffn_ln = g->mlp_norm_weights;
+    kp.hidden = g->hidden_states;
+    kp.silu = g->silu_out;
+    kp.queue_len = (int32_t)g->queue_len;
+    kp.num_layers = g->num_layers;
+    kp.H = g->hidden_size;
+    kp.F = g->intermediate_size;
+    kp.E = 1;
+    kp.bar_ops = (int32_t)g->bar_ops;
+    kp.bar_width = (int32_t)g->bar_width;
+    kp.expert_bs = g->up_gate_proj_block_size;
+    kp.down_bs = g->down_proj_block_size;
+    kp.oproj_bs = g->o_proj_block_size;
+    kp.eps = g->rms_norm_eps;
+    kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
+    kp.scratch = st->scratch;
+    kp.work_sharing = 0;
+    kp.red_cols = g->matvec_reduction_size;
+    kp.down_arrivals = (g->intermediate_size / g->matvec_reduction_size) * (g->hidden_size / g->down_proj_block_size);
+    kp.attn = 1;
+    AttnParams a{};
+    a.qkv = g->qkv_weights;
+    a.attn_ln = g->attn_norm_weights;
+    a.oproj = g->o_weights;
+    a.lm_norm = g->lm_head_norm_weights;
+    a.lm_head = g->lm_head_weights;
+    a.kc = g->k_cache;
+    a.vc = g->v_cache;
+    a.q_rope = g->q_post_rope;
+    a.attn_out = g->attn_out;
+    a.logits = g->logits;
+    a.rope_cos = g->rope_cos;
+    a.rope_sin = g->rope_sin;
+    a.lse_int = g->attn_lse_intermediates;
+    a.out_int = g->attn_out_intermediates;
+    a.Hq = g->num_attention_heads;
+    a.Hkv = g->num_kv_heads;
+    a.D = g->head_dim;
+    a.V = g->vocab_size;
+    a.T = g->kv_capacity;
+    a.P = g->attn_partial_slots;
+    a.qkv_bs = g->qkv_block_size;
+    a.kv_bs = g->attn_kv_block_size;
+    a.lm_bs = g->lm_head_block_size;
+    a.lm_red = g->hidden_size;
+    a.attn_scale = g->attn_scale;
+    a.skip_red = g->skip_attn_reduction ? 1 : 0;
+    a.kv_ring = kv_ring;
+    rc = upload_attn(st, a, reinterpret_cast<hipStream_t>(stream), &kp.ap);
+    if (rc != MK_OK) return rc;
+    kp.pos = g->pos_id;
+    return launch_persistent(reinterpret_cast<const void *>(mk_llama_kernel), st, g->num_workers, lds, kp,
+                             reinterpret_cast<hipStream_t>(stream));
+}
 
 int mk_mixtral_abi_version(void) { return MK_MIXTRAL_ABI_VERSION; }
 
@@ -1974,7 +2359,6 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const int kv_ring = kv_ring_for(g, (size_t)st->max_lds);
     if (kv_ring < 1) return MK_ERR_UNSUPPORTED;
     const size_t lds = lds_bytes_for(g, kv_ring);
-    int blocks = 0;
     // Mixtral's 8 experts get a kernel specialised for exactly 8
     const bool e8 = g->num_experts == 8;
     const bool attn = g->qkv_weights != nullptr;
@@ -1982,30 +2366,8 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
                                 : reinterpret_cast<const void *>(mk_mixtral_kernel<8, false>))
                         : (attn ? reinterpret_cast<const void *>(mk_mixtral_kernel<0, true>)
                                 : reinterpret_cast<const void *>(mk_mixtral_kernel<0, false>));
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds);
-    if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-    if (g->num_workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
-
-    // exit counter and work-sharing (cursor, done) per instruction slot
-    const size_t need = kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len;
-    if (need > st->scratch_ints) {
-        std::lock_guard<std::mutex> lock(g_mutex);
-        if (need > st->scratch_ints) {
-            size_t cap = st->scratch_ints ? st->scratch_ints : 4096;
-            while (cap < need) cap *= 2;
-            if (st->scratch != nullptr) {
-                // kernels queued earlier may still use the old buffer
-                if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-                if ((e = hipFree(st->scratch)) != hipSuccess) return hip_fail(e, "hipFree");
-                st->scratch = nullptr;
-                st->scratch_ints = 0;
-            }
-            if ((e = hipMalloc(reinterpret_cast<void **>(&st->scratch), cap * sizeof(int32_t))) != hipSuccess)
-                return hip_fail(e, "hipMalloc");
-            if ((e = hipMemset(st->scratch, 0, cap * sizeof(int32_t))) != hipSuccess) return hip_fail(e, "hipMemset");
-            st->scratch_ints = cap;
-        }
-    }
+    rc = ensure_scratch(st, kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len);
+    if (rc != MK_OK) return rc;
 
     KParams kp;
     kp.instructions = g->instructions;
@@ -2036,11 +2398,11 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.down_bs = g->down_proj_block_size;
     kp.oproj_bs = g->o_proj_block_size;
     kp.eps = g->rms_norm_eps;
-    const uint64_t us = g->spin_timeout_us ? g->spin_timeout_us : 2000000u;
-    const uint64_t ticks = us * kTicksPerUs;
-    kp.timeout_ticks = ticks > 0xffffffffu ? 0xffffffffu : (uint32_t)ticks;
+    kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
     kp.scratch = st->scratch;
     kp.work_sharing = g->work_sharing ? 1 : 0;
+    kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
+    kp.red_cols = 0;
     kp.attn = g->qkv_weights != nullptr;
     kp.ap = nullptr;
     if (kp.attn) {
@@ -2072,33 +2434,12 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
         a.attn_scale = g->attn_scale;
         a.skip_red = g->skip_attn_reduction ? 1 : 0;
         a.kv_ring = kv_ring;
-        if (st->attn == nullptr) {
-            std::lock_guard<std::mutex> lock(g_mutex);
-            if (st->attn == nullptr &&
-                (e = hipMalloc(reinterpret_cast<void **>(&st->attn), sizeof(AttnParams))) != hipSuccess)
-                return hip_fail(e, "hipMalloc");
-        }
-        // Copied only when it changes (a decode loop launches the same
-        // tensors every step); stream-ordered after the launches that read
-        // the previous contents.
-        if (std::memcmp(&a, &st->attn_host, sizeof(a)) != 0) {
-            if ((e = hipMemcpyAsync(st->attn, &a, sizeof(a), hipMemcpyHostToDevice,
-                                    reinterpret_cast<hipStream_t>(stream))) != hipSuccess)
-                return hip_fail(e, "hipMemcpyAsync");
-            st->attn_host = a;
-        }
-        kp.ap = st->attn;
+        rc = upload_attn(st, a, reinterpret_cast<hipStream_t>(stream), &kp.ap);
+        if (rc != MK_OK) return rc;
     }
     kp.pos = g->pos_id;
-
     // fn is one of the four instantiations above
-    void *args[] = {&kp};
-    e = hipLaunchKernel(fn, dim3((unsigned)g->num_workers), dim3(kThreads), args, lds,
-                        reinterpret_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel");
-    e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "hipGetLastError");
-    return MK_OK;
+    return launch_persistent(fn, st, g->num_workers, lds, kp, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mk_mixtral_read_status(int device, int32_t *out) {

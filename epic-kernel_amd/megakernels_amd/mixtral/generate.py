@@ -1,7 +1,7 @@
 """Greedy batch-1 decode driver over the persistent kernel.
 
-Counterpart of ``MK_Generator`` (``megakernels/generators.py:95-166``): a
-step embeds the input token into ``hidden_states``, refills the barrier
+Counterpart of ``MK_Generator`` (``megakernels/generators.py:95-166``), for
+the Mixtral VM and the dense Llama VM alike: a step embeds the input token into ``hidden_states``, refills the barrier
 tensor, sets ``pos_id``, zeroes the logits (the LM head accumulates its
 column blocks into them), launches the whole-model schedule once, and takes
 the argmax of the logits.  ``generate`` runs steps back to back, feeding each
@@ -37,13 +37,24 @@ class MK_Generator:
     def build(cls, model, prompt_len: int, mode: str = "rr", sm_count: int | None = None, **launch_kwargs):
         """Globals for ``model`` with the KV cache filled up to ``prompt_len``
         positions, the whole-model schedule assigned with ``mode``, and a
-        generator over it."""
-        globs = make_globals(model, seq_len=prompt_len, sm_count=sm_count)
+        generator over it.  The model type picks the VM: a model with
+        ``stacked_params.expert_gate`` is Mixtral, one with
+        ``stacked_params.gate_proj`` the dense Llama VM
+        (``megakernels/dispatch.py`` maps model types the same way)."""
+        if hasattr(model.stacked_params, "gate_proj"):
+            from ..latency.mk import LatencyMK_Interpreter
+            from ..latency.scheduler import make_dag as dag_fn
+            from ..latency.scheduler import make_globals as globals_fn
+
+            interpreter = LatencyMK_Interpreter()
+        else:
+            dag_fn, globals_fn, interpreter = make_dag, make_globals, MixtralMK_Interpreter()
+        globs = globals_fn(model, seq_len=prompt_len, sm_count=sm_count)
         globs.pos_id = prompt_len
-        nodes, end = make_dag(globs)
+        nodes, end = dag_fn(globs)
         schedule = Schedule(globs, nodes, end)
         tensorize_instructions(globs, assign_to_sms(mode, schedule=schedule))
-        return cls(model, MixtralMK_Interpreter(), schedule, **launch_kwargs)
+        return cls(model, interpreter, schedule, **launch_kwargs)
 
     def fill(self):
         self.schedule.globs.barriers.fill_(self.barrier_fill_val)

@@ -12,10 +12,9 @@ field order (hence the serialised word layout) are the reference's:
   7 Mixtral_RMS_LM_Head      [7, start_block, end_block, reduction_block]
   8 SpeculativeExpertPredict [8, layer]
 
-The HIP kernel executes opcodes 0 (NoOp), 5, 6 and 8 -- the MoE hot path.
-Opcodes 1-4 and 7 (attention and LM head) are defined so schedules built for
-the whole model serialise, but the kernel rejects them with
-``MK_ERR_UNSUPPORTED_OPCODE`` and the host refuses to launch them.
+The HIP kernel executes every opcode 0-8.  Opcodes 1-4 and 7 (attention and
+LM head) need the attention tensors; a launch without them (the MoE-only
+slice) rejects those opcodes with ``MK_ERR_UNSUPPORTED_OPCODE``.
 
 Two optional fields extend ``MixtralGlobals`` beyond the reference (both
 default to ``None``, which keeps the reference's semantics exactly):
@@ -45,9 +44,8 @@ OPCODE_EXPERT_DOWNPROJ_FUSED = 6
 OPCODE_RMS_LM_HEAD = 7
 OPCODE_SPECULATIVE_EXPERT_PREDICT = 8
 
-#: opcodes the HIP kernel implements (0 = NoOp)
-KERNEL_OPCODES = frozenset({0, OPCODE_RMS_ROUTER_UPGATE, OPCODE_EXPERT_DOWNPROJ_FUSED,
-                            OPCODE_SPECULATIVE_EXPERT_PREDICT})
+#: opcodes the HIP kernel implements (0 = NoOp); 1-4 and 7 need the attention tensors
+KERNEL_OPCODES = frozenset(range(9))
 
 
 @dataclass

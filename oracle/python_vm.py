@@ -275,6 +275,16 @@ def solve_qkv(globs: MixtralGlobals, ins: Mixtral_QKV):
     if layer > 0:
         bar = globs.barriers[layer - 1, ExpertDownProjFused.opcode() - 1]
         assert bar[0] == expected_downproj_barrier(globs), f"QKV layer {layer}: downproj barrier {int(bar[0])}"
+    qkv_rope_append(globs, ins)
+
+
+def qkv_rope_append(globs, ins) -> None:
+    """The body of the QKV opcode, shared by the Mixtral and dense VMs
+    (mkm/python_vm.py:70-118 = lat/python_vm.py:162-238): RMSNorm with the
+    attention norm, bf16 QKV rows, interleaved RoPE on q and k, q to
+    ``post_ln_rope_q``, k and v to the caches at ``pos_id``, one arrival per
+    block on its head's counter."""
+    layer = ins.layer_idx
     post_ln = rms_norm(globs.hidden_states, globs.attn_ln_weights[layer], globs.rms_norm_eps)
     pos = globs.pos_id
     D = globs.head_dim

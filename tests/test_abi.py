@@ -18,6 +18,7 @@ from megakernels_amd.scheduler import tensorize_instructions
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "mk_mixtral.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 @pytest.fixture(scope="module")
@@ -40,13 +41,63 @@ def test_header_declares_entry_points():
     assert sorted(mk_mixtral.EXPORTED_SYMBOLS) == names
 
 
+def all_declared_functions():
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mk_\w+)\s*\(", h.read_text(), re.M))
+    return sorted(names)
+
+
 def test_library_exports_every_declared_symbol(lib):
     out = subprocess.run(["nm", "-D", "--defined-only", str(mk_mixtral.library_path())],
                          capture_output=True, text=True, check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
-    for name in declared_functions():
+    names = all_declared_functions()
+    assert "mk_llama_launch" in names and "mk_mixtral_launch" in names
+    for name in names:
         assert name in exported, name
         assert hasattr(lib, name)
+
+
+def test_llama_header_entry_points_and_layout(tmp_path):
+    import mk_llama
+
+    text = (ROOT / "include" / "mk_llama.h").read_text()
+    declared = sorted(set(re.findall(r"^\s*\w+\s*(mk_llama_\w+)\s*\(", text, re.M)))
+    assert declared == sorted(mk_llama.EXPORTED_SYMBOLS)
+    fields = [f for f, _ in mk_llama.MkLlamaGlobals._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "mk_llama.h"\nint main(void) {\n'
+        '  printf("sizeof %zu\\n", sizeof(mk_llama_globals));\n'
+        + "".join(f'  printf("{f} %zu\\n", offsetof(mk_llama_globals, {f}));\n' for f in fields)
+        + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    lines = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True)
+                 .stdout.splitlines())
+    assert int(lines.pop("sizeof")) == ctypes.sizeof(mk_llama.MkLlamaGlobals)
+    for f in fields:
+        assert int(lines[f]) == getattr(mk_llama.MkLlamaGlobals, f).offset, f
+
+
+def test_llama_launch_validation_needs_no_gpu(lib):
+    import mk_llama
+
+    mk_llama.load_library()
+    assert lib.mk_llama_abi_version() == mk_llama.ABI_VERSION
+    assert lib.mk_llama_launch(None, None) == 1
+    g = mk_llama.MkLlamaGlobals()
+    g.struct_size = ctypes.sizeof(g)
+    g.abi_version = 99
+    assert lib.mk_llama_launch(ctypes.byref(g), None) == 1
+    g.abi_version = mk_llama.ABI_VERSION
+    assert lib.mk_llama_launch(ctypes.byref(g), None) == 1  # null tensors
+    with pytest.raises(TypeError):
+        mk_llama.mk_llama(1, 2, 3)
+    args = [torch.empty(0)] * 16 + [torch.empty(4, dtype=torch.bfloat16)] + [torch.empty(0)] * 6
+    with pytest.raises(ValueError, match="GPU"):
+        mk_llama.build_llama_struct(*args, 0, 1.0, 1e-5, False)
 
 
 def test_struct_layout_matches_header(tmp_path):
