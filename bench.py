@@ -239,24 +239,46 @@ def decode_bytes_per_token(cfg, seq_len: int) -> int:
     return 2 * (L * (attn + moe + kv) + V * H + H)
 
 
+def decode_bytes_per_token_llama(cfg, seq_len: int) -> int:
+    """Algorithmic HBM bytes of one dense (Llama) decode step: every layer's
+    QKV, O, up, gate and down projections with both norms, the K and V rows
+    of all cached positions, and the LM head with its norm (bf16)."""
+    L, H, F = cfg.num_hidden_layers, cfg.hidden_size, cfg.intermediate_size
+    Hq, Hkv, D, V = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.vocab_size
+    attn = (Hq + 2 * Hkv) * D * H + H * Hq * D + H
+    mlp = 3 * F * H + H
+    kv = 2 * seq_len * Hkv * D
+    return 2 * (L * (attn + mlp + kv) + V * H + H)
+
+
 def decode_bench(args):
-    """Whole-model greedy decode (BASELINE configs 4 and 5) through
-    MK_Generator: random-init Mixtral-8x7B-shaped weights resident in HBM,
-    a KV cache pre-filled with N(0, 1) to the context length, `decode_steps`
-    timed steps after `warmup` untimed ones."""
+    """Whole-model greedy decode through MK_Generator
+    (Llama-3.2-3B shape, 2048 cached positions, dense VM) and configs 4 and 5
+    (Mixtral-8x7B shape, 4096 / 16384 cached positions).  Random-init weights
+    resident in HBM, a KV cache pre-filled with N(0, 1) to the context
+    length, `decode_steps` timed steps after `warmup` untimed ones."""
     import torch
 
     from megakernels_amd.mixtral.generate import MK_Generator
     from megakernels_amd.mixtral.synthetic import C4, make_synthetic_mixtral
 
-    cfg = C4
-    prefill = 4096 if args.config == "c4" else 16384
-    steps, warmup = args.decode_steps, max(1, args.warmup)
+    llama = args.config == "c3"
+    if llama:
+        from megakernels_amd.latency.synthetic import C3, make_synthetic_llama
+
+        cfg, prefill = C3, 2048
+    else:
+        cfg, prefill = C4, (4096 if args.config == "c4" else 16384)
+    steps = args.decode_steps or (256 if llama else 128)
+    warmup = max(1, args.warmup)
     print(f"bench: building {args.config} ({cfg.num_hidden_layers} layers, {prefill} cached positions) on cuda:0",
           file=sys.stderr, flush=True)
     t0 = time.perf_counter()
-    model = make_synthetic_mixtral(cfg, "cuda", 0, full=True, kv_positions=prefill + steps + warmup + 1,
-                                   prefill=prefill, predictor_sigma=args.predict_sigma)
+    if llama:
+        model = make_synthetic_llama(cfg, "cuda", 0, kv_positions=prefill + steps + warmup + 1, prefill=prefill)
+    else:
+        model = make_synthetic_mixtral(cfg, "cuda", 0, full=True, kv_positions=prefill + steps + warmup + 1,
+                                       prefill=prefill, predictor_sigma=args.predict_sigma)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     gen = MK_Generator.build(model, prefill)
@@ -279,7 +301,7 @@ def decode_bench(args):
         save_record(args.trace, rec)
         print(format_report(rec), file=sys.stderr, flush=True)
     ms = secs / steps * 1e3
-    nbytes = decode_bytes_per_token(cfg, prefill + steps // 2)
+    nbytes = (decode_bytes_per_token_llama if llama else decode_bytes_per_token)(cfg, prefill + steps // 2)
     achieved = nbytes / (ms * 1e-3) / 1e9
     g = gen.schedule.globs
     out = {
@@ -296,9 +318,12 @@ def decode_bench(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"BASELINE config {'4' if args.config == 'c4' else '5'}: Mixtral-8x7B-shaped batch-1 greedy "
-                        f"decode (32 layers, 32/8 heads, head dim 128, 8 experts top-2, vocab 32000), KV cache "
-                        f"pre-filled to {prefill} positions, one persistent-kernel launch per token",
+            "workload": (f"BASELINE config 3: Llama-3.2-3B-shaped batch-1 greedy decode (28 layers, hidden 3072, "
+                         f"24/8 heads, head dim 128, FFN 8192, vocab 128256, RoPE theta 500000), KV cache pre-filled "
+                         f"to {prefill} positions, one persistent-kernel launch per token (dense VM)" if llama else
+                         f"BASELINE config {'4' if args.config == 'c4' else '5'}: Mixtral-8x7B-shaped batch-1 greedy "
+                         f"decode (32 layers, 32/8 heads, head dim 128, 8 experts top-2, vocab 32000), KV cache "
+                         f"pre-filled to {prefill} positions, one persistent-kernel launch per token"),
             "prefill": prefill,
             "workers": g.sm_count(),
             "attention_partitions": int(max(i.num_partials for i in gen.schedule.get_linear_instructions()
@@ -313,7 +338,7 @@ def decode_bench(args):
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
             "bytes_per_launch": nbytes,
-            "kernel": "mk_mixtral_kernel (whole model)",
+            "kernel": "mk_llama_kernel (whole model)" if llama else "mk_mixtral_kernel (whole model)",
         },
         "tokens_tail": tokens[0, -8:].tolist(),
     }
@@ -382,10 +407,12 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=1024)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c4", "c5"],
-                    help="c1/c2: one MoE layer per launch (c2 is the headline); c4/c5: whole-model greedy "
-                         "decode of the Mixtral-8x7B shape with 4096 / 16384 cached positions")
-    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c1/c2: one MoE layer per launch (c2 is the headline); c3: whole-model greedy decode of "
+                         "the Llama-3.2-3B shape (2048 cached positions); c4/c5: whole-model greedy decode of the "
+                         "Mixtral-8x7B shape with 4096 / 16384 cached positions")
+    ap.add_argument("--decode-steps", type=int, default=0,
+                    help="timed decode steps (default: 256 for c3, 128 for c4/c5, as BASELINE states them)")
     ap.add_argument("--predict-sigma", type=float, default=None,
                     help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
     ap.add_argument("--no-skewed", action="store_true")
@@ -423,7 +450,7 @@ def main():
 
     from megakernels_amd.mixtral.synthetic import C1, C2
 
-    if args.config in ("c4", "c5"):
+    if args.config in ("c3", "c4", "c5"):
         decode_bench(args)
         return
 

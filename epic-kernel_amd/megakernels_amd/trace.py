@@ -48,6 +48,17 @@ OPCODE_NAMES = {
     8: "SpeculativeExpertPredict",
 }
 
+#: opcode names of the dense (Llama) VM, megakernels/demos/latency/instructions.py
+DENSE_OPCODE_NAMES = {
+    1: "QKV",
+    2: "PartialAttn",
+    3: "AttnReduction",
+    4: "OProj",
+    5: "UpGateSiLU",
+    6: "DownProjResidual",
+    7: "RMS_LM_Head",
+}
+
 
 @dataclass
 class TimingRecord:
@@ -70,18 +81,29 @@ class TimingRecord:
     num_kv_heads: int = 0
     attn_kv_block_size: int = 0
     pos_id: int = 0
+    red_cols: int = 0  # dense VM: down-projection column chunk; 0 for Mixtral
+
+    @property
+    def dense(self) -> bool:
+        return self.red_cols > 0
+
+    @property
+    def opcode_names(self) -> dict:
+        return DENSE_OPCODE_NAMES if self.dense else OPCODE_NAMES
 
     @classmethod
     def from_globals(cls, globs) -> "TimingRecord":
+        dense = hasattr(globs, "up_gate_proj_block_size")
         return cls(
             timings=globs.timings.detach().cpu().numpy().copy(),
             instructions=globs.instructions.detach().cpu().numpy().copy(),
             hidden_size=globs.hidden_size,
             intermediate_size=globs.intermediate_size,
-            num_experts=globs.num_experts,
-            expert_proj_block_size=globs.expert_proj_block_size,
+            num_experts=1 if dense else globs.num_experts,
+            expert_proj_block_size=globs.up_gate_proj_block_size if dense else globs.expert_proj_block_size,
             down_proj_block_size=globs.down_proj_block_size,
-            k=globs.num_experts_per_tok,
+            k=1 if dense else globs.num_experts_per_tok,
+            red_cols=globs.matvec_reduction_size if dense else 0,
             qkv_block_size=globs.qkv_block_size,
             o_proj_block_size=globs.o_proj_block_size,
             lm_head_block_size=globs.lm_head_block_size,
@@ -118,6 +140,12 @@ class TimingRecord:
         ins = self.instructions[w, q]
         op = int(ins[0])
         H, F, E = self.hidden_size, self.intermediate_size, self.num_experts
+        if self.dense and op == 5:
+            return int(ins[2]) * self.expert_proj_block_size * H * 2 * 2  # gate + up rows of the listed blocks
+        if self.dense and op == 6:
+            return (int(ins[3]) - int(ins[2])) * self.down_proj_block_size * self.red_cols * 2
+        if self.dense and op == 7:
+            return (int(ins[2]) - int(ins[1])) * self.lm_head_block_size * H * 2
         if op == 5:
             rows = int(ins[3]) * self.expert_proj_block_size
             return self.k * 2 * rows * H * 2  # gate + up rows of each selected expert
@@ -151,13 +179,13 @@ def save_record(path, rec: TimingRecord) -> None:
         shape=np.array([rec.hidden_size, rec.intermediate_size, rec.num_experts,
                         rec.expert_proj_block_size, rec.down_proj_block_size, rec.k,
                         rec.qkv_block_size, rec.o_proj_block_size, rec.lm_head_block_size, rec.attn_width,
-                        rec.head_dim, rec.num_kv_heads, rec.attn_kv_block_size, rec.pos_id]))
+                        rec.head_dim, rec.num_kv_heads, rec.attn_kv_block_size, rec.pos_id, rec.red_cols]))
 
 
 def load_record(path) -> TimingRecord:
     d = np.load(Path(path), allow_pickle=False)
     shape = [int(x) for x in d["shape"]] + [0] * 8
-    return TimingRecord(d["timings"], d["instructions"], *shape[:14])
+    return TimingRecord(d["timings"], d["instructions"], *shape[:15])
 
 
 def barrier_waits(rec: TimingRecord) -> dict:
@@ -178,7 +206,7 @@ def barrier_waits(rec: TimingRecord) -> dict:
             wait = t[w, q, T_DONE_WAIT] - t[w, q, T_AT_WAIT]
             wait = 0.0 if np.isnan(wait) else max(0.0, float(wait))
             dur = max(0.0, float(t[w, q, T_END] - t[w, q, T_START]))
-            s = by_op.setdefault(op, {"name": OPCODE_NAMES.get(op, str(op)), "count": 0, "wait_us": 0.0,
+            s = by_op.setdefault(op, {"name": rec.opcode_names.get(op, str(op)), "count": 0, "wait_us": 0.0,
                                       "instr_us": 0.0})
             s["count"] += 1
             s["wait_us"] += wait
@@ -236,7 +264,7 @@ def phase_summary(rec: TimingRecord, percentiles=(0, 10, 50, 90, 100)) -> dict:
             v = t[:, :, slot][mask]
             v = v[~np.isnan(v)]
             if v.size:
-                out[(OPCODE_NAMES.get(op, str(op)), name)] = np.percentile(v, percentiles)
+                out[(rec.opcode_names.get(op, str(op)), name)] = np.percentile(v, percentiles)
     return out
 
 
@@ -281,7 +309,7 @@ def format_report(rec: TimingRecord, peak_gbs: float = 8000.0) -> str:
         lines.append(f"layer {show} stage windows (us, first start / last end):")
         for (lay, op), (a, b, _) in sorted(win.items()):
             if lay == show:
-                lines.append(f"  {OPCODE_NAMES.get(op, op):26s} {a:9.1f} {b:9.1f}  ({b - a:6.1f})")
+                lines.append(f"  {rec.opcode_names.get(op, op):26s} {a:9.1f} {b:9.1f}  ({b - a:6.1f})")
         ends = [max(b for (lay, _), (_, b, _) in win.items() if lay == L) for L in layers]
         if len(ends) > 2:
             lines.append(f"mean layer period {np.mean(np.diff(ends)):.1f} us over {len(layers)} layers")

@@ -112,3 +112,32 @@ def test_record_roundtrip_keeps_attention_fields(tmp_path):
     save_record(tmp_path / "r.npz", rec)
     back = load_record(tmp_path / "r.npz")
     assert (back.head_dim, back.num_kv_heads, back.attn_kv_block_size, back.pos_id) == (128, 8, 16, 4096)
+
+
+def test_dense_vm_byte_model_covers_each_weight_once():
+    """For the dense (Llama) VM the per-instruction byte model adds up to
+    each layer's up+gate, down and O/QKV weights, and the LM head, once."""
+    from megakernels_amd.latency.scheduler import make_dag, make_globals
+    from megakernels_amd.latency.synthetic import LLAMA_SMALL, make_synthetic_llama
+    from megakernels_amd.scheduler import Schedule, assign_to_sms, tensorize_instructions
+
+    model = make_synthetic_llama(LLAMA_SMALL, "cpu", 0, kv_positions=64, prefill=40)
+    g = make_globals(model, seq_len=40, sm_count=16)
+    g.pos_id = 40
+    tensorize_instructions(g, assign_to_sms("rr", schedule=Schedule(g, *make_dag(g))))
+    rec = TimingRecord.from_globals(g)
+    assert rec.dense and rec.red_cols == 512 and rec.opcode_names[6] == "DownProjResidual"
+    W, Q = rec.instructions.shape[:2]
+    by_op = {}
+    for w in range(W):
+        for q in range(Q):
+            op = int(rec.instructions[w, q, 0])
+            by_op[op] = by_op.get(op, 0) + rec.streamed_bytes(w, q)
+    c = LLAMA_SMALL
+    L, H, F, D = c.num_hidden_layers, c.hidden_size, c.intermediate_size, c.head_dim
+    assert by_op[5] == L * 2 * F * H * 2
+    assert by_op[6] == L * H * F * 2
+    assert by_op[7] == c.vocab_size * H * 2
+    assert by_op[1] == L * (c.num_attention_heads + 2 * c.num_key_value_heads) * D * H * 2
+    assert by_op[4] == L * H * c.num_attention_heads * D * 2
+    assert by_op[2] == L * c.num_key_value_heads * 41 * 2 * D * 2
