@@ -588,6 +588,16 @@ __device__ __forceinline__ int next_local_item(SharedState &sh, int lane) {
     return __builtin_amdgcn_readfirstlane(v);
 }
 
+// silu_out[e][r] = bf16(bf16(silu(bf16 g)) * bf16 u) from the wave sums of
+// the gate and up rows (lane 0 stores).
+__device__ __forceinline__ void silu_store(const KParams &p, int e, int r, float ag, float au, int lane) {
+    if (lane == 0) {
+        const float g = rbf(ag), u = rbf(au);
+        const float sg = rbf(g / (1.0f + expf(-g)));
+        st_dev16(p.silu + (size_t)e * p.F + r, f2bf(sg * u));
+    }
+}
+
 // One item of opcode 5: row r of the FFN dimension for expert slot j, i.e.
 // the gate and up rows (H bf16 each) dotted with the normed hidden state,
 // then silu_out[e][r] = bf16(bf16(silu(bf16(g))) * bf16(u)).
@@ -599,13 +609,7 @@ __device__ __forceinline__ void upgate_item(const KParams &p, const u32x4 *act, 
     const size_t off = ((size_t)(layer * p.E + e) * p.F + r) * (size_t)p.H;
     float ag = 0.f, au = 0.f;
     dot_pair(p.gate + off, p.up + off, act, act, p.H / kChunkElems, lane, ag, au);
-    ag = wave_sum(ag);
-    au = wave_sum(au);
-    if (lane == 0) {
-        const float g = rbf(ag), u = rbf(au);
-        const float sg = rbf(g / (1.0f + expf(-g)));
-        st_dev16(p.silu + (size_t)e * p.F + r, f2bf(sg * u));
-    }
+    silu_store(p, e, r, wave_sum(ag), wave_sum(au), lane);
 }
 
 // Wave-level claim of the next item of an instruction.  Lane 0 issues the
@@ -1398,6 +1402,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
             vn = ld_dev128(vbase, off);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging has landed in LDS
+        if (r == 0) stamp(tim, MK_TEVENT_FIRST_USE);
         if (patch && first + c_new * CT == pos) {
             const int k = c_new - r * nb;
             kl[k * (kKvChunkBytes / 16)] = kn;
@@ -1459,6 +1464,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
         }
     }
 
+    stamp(tim, MK_TEVENT_AT_GMEM_STORE);  // wave 0's positions done
     // fold the token slots of the wave (lanes with the same dp) to the wave max
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
@@ -1735,17 +1741,50 @@ __device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &s
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int items = n * p.expert_bs, nc = p.H / kChunkElems;
+    // each wave's first item (its gate and up rows) is loaded before the
+    // wait: the weights do not depend on it
+    PairAhead pre;
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    if (wave < items) {
+        const int k = wave / p.expert_bs;
+        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + wave - k * p.expert_bs;
+        const size_t off = ((size_t)layer * p.F + row) * (size_t)p.H;
+        const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
+        const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
+#pragma unroll
+        for (int i = 0; i < kAheadChunks; ++i)
+            if (i < nc) {
+                pre.a[i] = load_stream(wg + i * 64);
+                pre.b[i] = load_stream(wu + i * 64);
+            }
+    }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, p.ffn_ln + (size_t)layer * p.H);
-    stamp(tim, MK_TEVENT_FIRST_LOAD);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int items = n * p.expert_bs;
-    for (int it = wave; it < items; it = next_local_item(sh, lane)) {
+    if (wave < items) {  // the item loaded ahead
+        const int k = wave / p.expert_bs;
+        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + wave - k * p.expert_bs;
+        float ag = 0.f, au = 0.f;
+#pragma unroll
+        for (int i = 0; i < kAheadChunks; ++i)
+            if (i < nc) {
+                ag = dot8(pre.a[i], act[i * 64 + lane], ag);
+                au = dot8(pre.b[i], act[i * 64 + lane], au);
+            }
+        if (nc > kAheadChunks) {
+            const size_t off = ((size_t)layer * p.F + row) * (size_t)p.H + kAheadChunks * kChunkElems;
+            dot_pair(p.gate + off, p.up + off, act + kAheadChunks * 64, act + kAheadChunks * 64, nc - kAheadChunks,
+                     lane, ag, au);
+        }
+        silu_store(p, 0, row, wave_sum(ag), wave_sum(au), lane);
+    }
+    for (int it = next_local_item(sh, lane); it < items; it = next_local_item(sh, lane)) {
         const int k = it / p.expert_bs;
-        const int b = __builtin_amdgcn_readfirstlane(ins[3 + k]);
-        upgate_item(p, act, layer, b * p.expert_bs, p.expert_bs, 0, 0, it - k * p.expert_bs, lane);
+        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + it - k * p.expert_bs;
+        upgate_item(p, act, layer, row, 1, 0, 0, 0, lane);
     }
     drain_and_sync();
     arrive(bar_at(p, layer, 5), n);
@@ -1753,54 +1792,89 @@ __device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &s
     return true;
 }
 
+// NR rows x NC chunks of a row-major bf16 matrix (row stride ld, columns
+// from col0), 16 bytes per lane per (row, chunk): all NR * NC loads are
+// issued before any is used.
+template <int NR, int NC>
+__device__ __forceinline__ void load_rows(u32x4 (&w)[NR][NC], const uint16_t *mat, size_t ld, int row, int col0,
+                                          int lane) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            w[i][c] = load_stream(reinterpret_cast<const u32x4 *>(mat + (size_t)(row + i) * ld + col0) + c * 64 + lane);
+}
+
 // Opcode 6, DownProjResidual [6, layer, start, end, red]: rows
 // [start, end) * down_proj_block_size of the down projection, columns
 // [red, red + 1) * red_cols, dotted with those columns of silu_out; each row
 // pair is added into hidden with one packed bf16 atomic (the column chunks
 // of a row run on different workgroups), h = bf16(h + bf16(partial)).
-// Arrival end - start on [l][5][0].
-__device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
-                                              const Ctx &c, int32_t *tim) {
-    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
-    const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
-    const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
-    const int red = __builtin_amdgcn_readfirstlane(ins[4]);
-    const int R = p.red_cols;
-    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.down_bs > p.H || red < 0 ||
-        (int64_t)(red + 1) * R > p.F) {
-        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 6, layer, b0, red);
-        return false;
-    }
-    if (threadIdx.x == 0) sh.next_item = kWaves;
+// Arrival end - start on [l][5][0].  Items are NR rows x NC = red_cols / 512
+// chunks (16 loads per lane); each wave's first item is loaded before the
+// wait on opcode 5, since the weights do not depend on it.
+template <int NR, int NC>
+__device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+                                                int32_t *tim, int layer, int b0, int b1, int red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int R = p.red_cols, col0 = red * R;
+    const int r0 = b0 * p.down_bs, nitems = (b1 - b0) * p.down_bs / NR;
+    const uint16_t *wm = p.down + (size_t)layer * p.H * p.F;
+    u32x4 w[NR][NC];
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    if (wave < nitems) load_rows<NR, NC>(w, wm, (size_t)p.F, r0 + wave * NR, col0, lane);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    const int col0 = red * R;
-    for (int v = threadIdx.x; v < (R >> 3); v += kThreads)
-        act[v] = ld_dev128(p.silu, (uint32_t)(col0 + v * 8) * 2u);
+    for (int v = threadIdx.x; v < (R >> 3); v += kThreads) act[v] = ld_dev128(p.silu, (uint32_t)(col0 + v * 8) * 2u);
     __syncthreads();
-    stamp(tim, MK_TEVENT_FIRST_LOAD);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = b0 * p.down_bs, nrows = (b1 - b0) * p.down_bs;
-    const uint16_t *w = p.down + (size_t)layer * p.H * p.F;
-    for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
-        const int ra = r0 + 2 * it;
-        float aa = 0.f, ab = 0.f;
-        dot_pair(w + (size_t)ra * p.F + col0, w + (size_t)(ra + 1) * p.F + col0, act, act, R / kChunkElems, lane,
-                 aa, ab);
-        aa = wave_sum(aa);
-        ab = wave_sum(ab);
+    for (int it = wave; it < nitems; it = next_local_item(sh, lane)) {
+        const int row = r0 + it * NR;
+        if (it != wave) load_rows<NR, NC>(w, wm, (size_t)p.F, row, col0, lane);
+        float acc[NR];
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            acc[i] = 0.f;
+#pragma unroll
+            for (int k = 0; k < NC; ++k) acc[i] = dot8(w[i][k], act[k * 64 + lane], acc[i]);
+            acc[i] = wave_sum(acc[i]);
+        }
         if (lane == 0) {
-            const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(aa)),
-                                __builtin_bit_cast(__bf16, (uint16_t)f2bf(ab))};
-            __builtin_amdgcn_global_atomic_fadd_v2bf16((__attribute__((address_space(1))) bf16x2_t *)(p.hidden + ra),
-                                                       v);
+#pragma unroll
+            for (int i = 0; i < NR; i += 2) {
+                const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(acc[i])),
+                                    __builtin_bit_cast(__bf16, (uint16_t)f2bf(acc[i + 1]))};
+                __builtin_amdgcn_global_atomic_fadd_v2bf16(
+                    (__attribute__((address_space(1))) bf16x2_t *)(p.hidden + row + i), v);
+            }
         }
     }
     drain_and_sync();
     arrive(bar_at(p, layer, 6), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
+}
+
+__device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+                                              const Ctx &c, int32_t *tim) {
+    const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
+    const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
+    const int red = __builtin_amdgcn_readfirstlane(ins[4]);
+    if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.down_bs > p.H || red < 0 ||
+        (int64_t)(red + 1) * p.red_cols > p.F) {
+        report_error(p, MK_ERR_BAD_INSTRUCTION, c, 6, layer, b0, red);
+        return false;
+    }
+    if (threadIdx.x == 0) sh.next_item = kWaves;
+    // the host admits red_cols of 1, 2, 4 or 8 chunks and even block sizes
+    // that the row group divides
+    switch (p.red_cols / kChunkElems) {
+    case 1: return dense_down_rows<16, 1>(p, sh, act, c, tim, layer, b0, b1, red);
+    case 2: return dense_down_rows<8, 2>(p, sh, act, c, tim, layer, b0, b1, red);
+    case 4: return dense_down_rows<4, 4>(p, sh, act, c, tim, layer, b0, b1, red);
+    default: return dense_down_rows<2, 8>(p, sh, act, c, tim, layer, b0, b1, red);
+    }
 }
 
 // Opcode 7, RMS_LM_Head [7, start, end]: RMSNorm with the LM-head norm, then
@@ -2204,6 +2278,10 @@ int validate_llama(const mk_llama_globals *g) {
     if (g->bar_width < Hq + 2 * Hkv) return MK_ERR_INVALID_ARGUMENT;
     const int R = g->matvec_reduction_size;
     if (R < kChunkElems || R % kChunkElems || F % R) return MK_ERR_UNSUPPORTED;
+    // opcode 6 takes items of 16 / (R / 512) rows x R / 512 chunks
+    const int rc = R / kChunkElems;
+    if (rc != 1 && rc != 2 && rc != 4 && rc != 8) return MK_ERR_UNSUPPORTED;
+    if (g->down_proj_block_size % (16 / rc)) return MK_ERR_UNSUPPORTED;
     if (g->up_gate_proj_block_size < 1 || F % g->up_gate_proj_block_size || g->down_proj_block_size < 2 ||
         g->down_proj_block_size % 2 || H % g->down_proj_block_size || g->o_proj_block_size < 2 ||
         g->o_proj_block_size % 2 || H % g->o_proj_block_size)

@@ -44,16 +44,19 @@ BARRIER_OPS = 10
 
 
 def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 0,
-                 sm_count: int | None = None) -> Globals:
+                 sm_count: int | None = None, attention_partitions: str = "mi355x") -> Globals:
     """Activation buffers plus ``model``'s stacked weights (duck-typed like
     the reference's ``LlamaForCausalLM``); ``sm_count`` overrides the device
-    query (needed when the globals live on the CPU)."""
+    query (needed when the globals live on the CPU); ``attention_partitions``
+    is the split-KV partition policy (the Mixtral scheduler's
+    ``pick_num_attention_partitions``; ``"reference"`` reproduces the
+    reference's instruction list)."""
     cfg = model.config
     device = torch.device(model.device)
     dtype = model.dtype
     workers = sm_count if sm_count is not None else get_sm_count(device)
     if skip_attn_reduction is None:
-        parts = pick_num_attention_partitions(seq_len + 1, 0, cfg.num_key_value_heads, workers)
+        parts = pick_num_attention_partitions(seq_len + 1, 0, cfg.num_key_value_heads, workers, attention_partitions)
         skip_attn_reduction = parts == 1
     sp = model.stacked_params
     Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -105,6 +108,7 @@ def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 
         attn_reduction_size=Hq // Hkv,
     )
     globs.sm_count_override = sm_count
+    globs.attn_partition_policy = attention_partitions
     return globs
 
 
@@ -178,7 +182,9 @@ def make_dag(globs: Globals, stop_after_op: str | None = None, layer_limit: int 
 
 
 def make_dag_layer(globs: Globals, layer_idx: int, prev_layer_outputs, stop_after_op: str | None = None):
-    parts = pick_num_attention_partitions(globs.pos_id + 1, 0, globs.num_kv_heads, globs.sm_count())
+    parts = pick_num_attention_partitions(globs.pos_id + 1, 0, globs.num_kv_heads, globs.sm_count(),
+                                          getattr(globs, "attn_partition_policy", "reference"),
+                                          globs.attn_kv_block_size)
     globs.skip_attn_reduction = parts == 1
     nodes: list[DAG_Node] = []
 

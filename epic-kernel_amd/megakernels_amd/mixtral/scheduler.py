@@ -21,6 +21,12 @@ Differences, all MI355X-motivated and recorded here:
   exactly 7 blocks per worker, where 16-row blocks leave a 4-vs-3 imbalance.
   Passing ``16`` reproduces the reference partition.  The oracle reads the
   block sizes from the globals, so results do not depend on this choice.
+* the split-KV partition count defaults to the MI355X policy of
+  :func:`pick_num_attention_partitions` (chunks of >= 64 positions, up to 25
+  partitions per KV head) instead of the reference's (>= 256 positions, at
+  most 160 / kv_heads): the kernel's partial attention is VALU-bound per
+  workgroup, so more, shorter partitions finish sooner.
+  ``attention_partitions="reference"`` reproduces the reference partition.
 * ``make_moe_dag`` builds the MoE-only slice of one layer (optional opcode 8,
   then opcode 5 and opcode 6) for running the hot path in isolation; the
   attention prefix it skips is represented by pre-filling the O-proj barrier
@@ -53,14 +59,35 @@ from .instructions import (
 BARRIER_OPS = 10
 #: reference cap on attention partitions per layer (mkm/scheduler.py:21)
 ATTN_PARTITION_CAP = 160
+#: partials a terminal reduction can list: its 32-word instruction holds 7
+#: other words
+MAX_REDUCTION_LIST = 25
 
 
-def pick_num_attention_partitions(prompt_len: int, ntok: int, num_kv_heads: int, sm_count: int) -> int:
-    """Split-KV partition count: chunks of at least 256 tokens, at most
-    ``min(W, 160) // kv_heads`` partitions (mkm/scheduler.py:24-32)."""
-    chunks = math.ceil((prompt_len + ntok) / 256)
-    cap = min(sm_count, ATTN_PARTITION_CAP) // num_kv_heads
-    return max(1, min(chunks, cap))
+def pick_num_attention_partitions(prompt_len: int, ntok: int, num_kv_heads: int, sm_count: int,
+                                  policy: str = "reference", kv_block_size: int = 16) -> int:
+    """Split-KV partition count.
+
+    ``"reference"`` (mkm/scheduler.py:24-32): chunks of at least 256
+    positions, at most ``min(W, 160) // kv_heads`` partitions.
+
+    ``"mi355x"``: chunks of at least 64 positions and at most ``min(W //
+    kv_heads, 25)`` partitions, trimmed so that none is empty.  The kernel's
+    partial attention is bound by its VALU work per workgroup (positions x
+    query heads per KV head), not by bandwidth, so on 256 compute units it
+    pays to spread the cache over more of them; 25 is what one terminal
+    reduction instruction can list.
+    """
+    seq = prompt_len + ntok
+    if policy == "reference":
+        chunks = math.ceil(seq / 256)
+        cap = min(sm_count, ATTN_PARTITION_CAP) // num_kv_heads
+        return max(1, min(chunks, cap))
+    if policy != "mi355x":
+        raise ValueError(f"unknown partition policy {policy!r}")
+    n = max(1, min(math.ceil(seq / 64), sm_count // num_kv_heads, MAX_REDUCTION_LIST))
+    total = math.ceil(seq / kv_block_size)
+    return max(1, math.ceil(total / math.ceil(total / n)))
 
 
 def pick_block_size(rows: int, workers: int, candidates=(16, 8, 4)) -> int:
@@ -88,6 +115,7 @@ def make_globals(
     sm_count: int | None = None,
     expert_proj_block_size: int | None = None,
     down_proj_block_size: int | None = None,
+    attention_partitions: str = "mi355x",
 ) -> MixtralGlobals:
     """Allocate activation buffers and wrap ``model``'s stacked weights.
 
@@ -97,7 +125,10 @@ def make_globals(
     ``expert_gate``, ``expert_up``, ``expert_down``), ``.lm_head.input_norm.
     weight``, ``.lm_head.lm_head.weight``, ``.stacked_kv_cache`` and
     ``.model.rope_cos/rope_sin``.  ``sm_count`` overrides the device query
-    (needed when the globals live on the CPU).
+    (needed when the globals live on the CPU).  ``attention_partitions``
+    picks the split-KV partition policy of ``make_dag``
+    (:func:`pick_num_attention_partitions`; ``"reference"`` reproduces the
+    reference's instruction list).
     """
     cfg = model.config
     device = torch.device(model.device)
@@ -106,7 +137,7 @@ def make_globals(
     workers = sm_count if sm_count is not None else get_sm_count(device)
 
     if skip_attn_reduction is None:
-        parts = pick_num_attention_partitions(seq_len + 1, 0, cfg.num_key_value_heads, workers)
+        parts = pick_num_attention_partitions(seq_len + 1, 0, cfg.num_key_value_heads, workers, attention_partitions)
         skip_attn_reduction = parts == 1
 
     def buf(shape, buf_dtype=dtype):
@@ -180,6 +211,7 @@ def make_globals(
         predictor_weights=getattr(sp, "predictor_weight", None),
     )
     globs.sm_count_override = sm_count
+    globs.attn_partition_policy = attention_partitions
     return globs
 
 
@@ -249,7 +281,9 @@ def make_dag(globs: MixtralGlobals, stop_after_op: str | None = None, layer_limi
 
 
 def make_dag_layer(globs: MixtralGlobals, layer_idx: int, prev_layer_outputs, stop_after_op: str | None = None):
-    parts = pick_num_attention_partitions(globs.pos_id + 1, 0, globs.num_kv_heads, globs.sm_count())
+    parts = pick_num_attention_partitions(globs.pos_id + 1, 0, globs.num_kv_heads, globs.sm_count(),
+                                          getattr(globs, "attn_partition_policy", "reference"),
+                                          globs.attn_kv_block_size)
     globs.skip_attn_reduction = parts == 1
     nodes: list[DAG_Node] = []
 

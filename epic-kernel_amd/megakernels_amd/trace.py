@@ -7,9 +7,10 @@ convention (``include/util.cuh:220-252``):
 
 * 0 / 4    instruction start / end
 * 44 / 45  barrier wait entered / satisfied
-* 46       own items done (work sharing)
+* 46       own items done (work sharing; opcode 2: wave 0's positions)
 * 47       instruction's stores complete and arrival made
 * 48       first weight load issued
+* 49       first staged data in place (opcode 2: its K/V ring has landed)
 
 This module turns that record into what the reference's plotting scripts
 derive from theirs, as numbers rather than figures:
@@ -35,7 +36,7 @@ import numpy as np
 TICKS_PER_US = 100.0
 T_START, T_END = 0, 4
 T_AT_WAIT, T_DONE_WAIT = 44, 45
-T_OWN_DONE, T_DONE_STORE, T_FIRST_LOAD = 46, 47, 48
+T_OWN_DONE, T_DONE_STORE, T_FIRST_LOAD, T_FIRST_USE = 46, 47, 48, 49
 
 OPCODE_NAMES = {
     1: "QKV",
@@ -255,8 +256,8 @@ def phase_summary(rec: TimingRecord, percentiles=(0, 10, 50, 90, 100)) -> dict:
     (opcode name, event)."""
     t = rec.micros()
     ops = rec.instructions[:, :, 0]
-    events = {"start": T_START, "wait_done": T_DONE_WAIT, "first_load": T_FIRST_LOAD, "done": T_DONE_STORE,
-              "end": T_END}
+    events = {"start": T_START, "wait_done": T_DONE_WAIT, "first_load": T_FIRST_LOAD, "first_use": T_FIRST_USE,
+              "own_done": T_OWN_DONE, "done": T_DONE_STORE, "end": T_END}
     out = {}
     for op in sorted(set(int(x) for x in np.unique(ops)) - {0}):
         mask = ops == op

@@ -100,14 +100,15 @@ def test_make_globals_buffers():
     assert g.skip_attn_reduction  # 21 positions: one partition
 
 
-def test_dag_structure():
+@pytest.mark.parametrize("policy,parts", [("reference", 2), ("mi355x", 4)])
+def test_dag_structure(policy, parts):
     model = make_synthetic_llama(LLAMA_SMALL, "cpu", 0, kv_positions=400, prefill=300)
-    g = make_globals(model, seq_len=300, sm_count=16)
+    g = make_globals(model, seq_len=300, sm_count=16, attention_partitions=policy)
     g.pos_id = 300
     nodes, end = make_dag(g)
     ops = [n.instruction.opcode() for n in nodes]
     per_layer = {op: ops.count(op) // 2 for op in range(1, 7)}
-    assert per_layer[2] == 4 * 2 and per_layer[3] == 4  # two partitions per KV head, one reduction each
+    assert per_layer[2] == 4 * parts and per_layer[3] == 4  # partitions per KV head, one reduction each
     assert per_layer[4] == 1536 // 16
     assert ops.count(7) == 16
     # every opcode-5 node depends on all O-proj nodes of its layer; opcode 6 on all opcode-5 nodes
@@ -116,3 +117,23 @@ def test_dag_structure():
     down0 = [n for n in nodes if n.instruction.opcode() == 6 and n.instruction.layer_idx == 0]
     assert all(set(map(id, n.dependencies)) == set(map(id, up0)) for n in down0)
     assert expected_downproj_arrivals(g) == 4 * (1536 // 16)
+
+
+@pytest.mark.parametrize("seq,kv,W", [(1, 8, 256), (64, 8, 256), (65, 8, 256), (2049, 8, 256), (4097, 8, 256),
+                                      (16385, 8, 256), (301, 4, 16), (1000, 2, 7)])
+def test_mi355x_partition_policy(seq, kv, W):
+    """At most min(W / kv, 25) partitions, none empty, more than 32
+    positions each on average (n = ceil(seq / 64) before the cap); the
+    reference policy is unchanged."""
+    from megakernels_amd.mixtral.scheduler import pick_num_attention_partitions
+    from oracle.python_vm import partial_token_range
+
+    n = pick_num_attention_partitions(seq, 0, kv, W, "mi355x")
+    assert 1 <= n <= max(1, min(W // kv, 25))
+    ranges = [partial_token_range(seq, 16, n, p) for p in range(n)]
+    assert all(b > a for a, b in ranges)
+    assert [t for a, b in ranges for t in range(a, b)] == list(range(seq))
+    if n < min(W // kv, 25):
+        assert n == 1 or seq / n > 32
+    ref = pick_num_attention_partitions(seq, 0, kv, W)
+    assert ref == max(1, min(math.ceil(seq / 256), min(W, 160) // kv))
