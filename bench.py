@@ -281,7 +281,8 @@ def decode_bench(args):
                                        prefill=prefill, predictor_sigma=args.predict_sigma)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
-    gen = MK_Generator.build(model, prefill, mode=args.assign)
+    gen = MK_Generator.build(model, prefill, mode=args.assign,
+                             dag_kwargs=None if llama else {"predict": not args.no_predict})
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
@@ -329,6 +330,7 @@ def decode_bench(args):
             "attention_partitions": int(max(i.num_partials for i in gen.schedule.get_linear_instructions()
                                             if i.opcode() == 2)),
             "predictor_sigma": args.predict_sigma,
+            "predictor": None if llama else not args.no_predict,
             "assignment": args.assign,
         },
         "roofline": {
@@ -416,6 +418,8 @@ def main():
                     help="timed decode steps (default: 256 for c3, 128 for c4/c5, as BASELINE states them)")
     ap.add_argument("--assign", default="rr", choices=["rr", "zz", "wave", "dag"],
                     help="c3/c4/c5: instruction-to-worker assignment of the whole-model schedule")
+    ap.add_argument("--no-predict", action="store_true",
+                    help="c4/c5: leave opcode 8 (expert prediction) and the early expert loads that use it out")
     ap.add_argument("--predict-sigma", type=float, default=None,
                     help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
     ap.add_argument("--no-skewed", action="store_true")

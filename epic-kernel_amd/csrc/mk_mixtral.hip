@@ -79,6 +79,12 @@
 #define MK_PF_ROUNDS 1
 #endif
 
+// Opcode-5 items per wave warmed into L2 from opcode 8's prediction before
+// the O-proj wait (whole-model launches).
+#ifndef MK_SPEC_ITEMS
+#define MK_SPEC_ITEMS 1
+#endif
+
 namespace {
 
 constexpr int kThreads = MK_THREADS;
@@ -101,6 +107,8 @@ constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 
 static_assert(kThreads % 64 == 0 && kThreads <= 1024, "wave64 workgroup");
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;          // LDS pointer (global_load_lds destination)
+typedef const __attribute__((address_space(1))) void global_void_t;  // global pointer (global_load_lds source)
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct KParams {
@@ -169,6 +177,7 @@ struct SharedState {
     int pool_n;
     int wave_cnt[kWaves];
     int pool_slot[kMaxPoolIns], pool_row0[kMaxPoolIns], pool_nrows[kMaxPoolIns];
+    int spec_e[2];  // opcode 5: experts opcode 8 predicted for the layer (-1: none yet)
 };
 
 struct Ctx {
@@ -416,6 +425,35 @@ __device__ __forceinline__ void dot_pair(const uint16_t *row_a, const uint16_t *
     case 1: dot_pair_n<1>(wa + c * 64, wb + c * 64, xa + c * 64, xb + c * 64, acc_a, acc_b); break;
     default: break;
     }
+}
+
+// The first item of a wave in matvec_rows (rows r0 + 2 * wave and the next),
+// first min(nc, 8) chunks, loaded ahead: issued before a wait on inputs that
+// the weights do not depend on, so the weight stream overlaps the wait.
+constexpr int kAheadChunks = 8;
+struct PairAhead {
+    u32x4 a[kAheadChunks], b[kAheadChunks];
+};
+
+__device__ __forceinline__ void pair_ahead_load(PairAhead &r, const uint16_t *mat, size_t ld, int col0, int nc,
+                                                int r0, int nrows) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (2 * wave >= nrows) return;
+    const int ra = r0 + 2 * wave;
+    const u32x4 *wa = reinterpret_cast<const u32x4 *>(mat + (size_t)ra * ld + col0) + lane;
+    const u32x4 *wb = reinterpret_cast<const u32x4 *>(mat + (size_t)(ra + 1) * ld + col0) + lane;
+#pragma unroll
+    for (int i = 0; i < kAheadChunks; ++i)
+        if (i < nc) {
+            r.a[i] = load_stream(wa + i * 64);
+            r.b[i] = load_stream(wb + i * 64);
+        }
+}
+
+// Byte offset in the dynamic LDS of the 8 KiB (1 KiB per wave) that the
+// opcode-6 cache warming writes into: after the SiLU staging area.
+__device__ __forceinline__ uint32_t lds_prefetch_offset(const KParams &p) {
+    return (uint32_t)p.F * 4u;
 }
 
 // ---------------------------------------------------------------------------
@@ -738,9 +776,9 @@ __device__ __forceinline__ void steal_upgate(const KParams &p, const SharedState
     }
 }
 
-template <int kE>
+template <int kE, bool kSpec>
 __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
-                                     const Ctx &c, int32_t *tim) {
+                                                     const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
     const int nb = __builtin_amdgcn_readfirstlane(ins[3]);
@@ -758,6 +796,44 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     if (threadIdx.x == 0) sh.next_item = kWaves;
     // the pool's instruction list does not depend on the producers either
     if (p.work_sharing) pool_scan(p, sh, layer, c.worker / kPoolGroup);
+    const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
+    // Speculative early loads (whole-model launches, the reference's
+    // mx/rms_router_matvec.cu:259-290 re-expressed): once opcode 8 has
+    // predicted this layer's experts (checked, never waited for), each wave
+    // warms its first MK_SPEC_ITEMS items of the predicted top-1 expert into
+    // L2 (global_load_lds into an LDS sink: no registers held across the
+    // wait) before the O-proj wait.  A wrong prediction only costs the loads.
+    // More than one item per wave (128 KiB per CU, the CU's share of its
+    // XCD's L2) measured slower.
+    if constexpr (kSpec) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (threadIdx.x == 0) {
+            int e0 = -1, e1 = -1;
+            if (!p.work_sharing && (int)ld_dev32(bar_at(p, layer, 8)) >= 1) {
+                e0 = (int)ld_dev32(p.pred_idx);
+                e1 = (int)ld_dev32(p.pred_idx + 1);
+                if (e0 < 0 || e0 >= p.E || e1 < 0 || e1 >= p.E) e0 = e1 = -1;
+            }
+            sh.spec_e[0] = e0;
+            sh.spec_e[1] = e1;
+        }
+        __syncthreads();
+        const int pe0 = __builtin_amdgcn_readfirstlane(sh.spec_e[0]);
+        if (pe0 >= 0) {
+            stamp(tim, MK_TEVENT_FIRST_USE);
+            lds_void_t *sink = (lds_void_t *)(act + (lds_prefetch_offset(p) >> 4) + wave * 64);
+            const int nc = p.H / kChunkElems;
+            for (int it = wave; it < nrows && it < MK_SPEC_ITEMS * kWaves; it += kWaves) {
+                const size_t off = ((size_t)(layer * p.E + pe0) * p.F + row0 + it) * (size_t)p.H;
+                const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
+                const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
+                for (int i = 0; i < nc; ++i) {
+                    __builtin_amdgcn_global_load_lds((global_void_t *)(wg + i * 64), sink, 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((global_void_t *)(wu + i * 64), sink, 16, 0, 0);
+                }
+            }
+        }
+    }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
@@ -765,6 +841,12 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     float logits[Experts<kE>::kMax];
     rms_router<kE>(p, sh, act, layer, p.router, rr, tim, logits);
     const Top2 t = softmax_top2<kE>(p, logits);
+    if constexpr (kSpec) {
+        // predicted and selected experts, one byte each (0xff: no prediction)
+        if (tim != nullptr && threadIdx.x == 0)
+            tim[MK_TEVENT_PREDICTION] = (int32_t)((uint32_t)(sh.spec_e[0] & 0xff) | ((uint32_t)(sh.spec_e[1] & 0xff) << 8) |
+                                                  ((uint32_t)t.i0 << 16) | ((uint32_t)t.i1 << 24));
+    }
     const float psum = t.p0 + t.p1;
     const uint32_t sc0 = f2bf(t.p0 / psum), sc1 = f2bf(t.p1 / psum);
     const int tid = threadIdx.x;
@@ -790,7 +872,6 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
     const int lane = tid & 63, wave = tid >> 6;
-    const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
     if (p.work_sharing && sh.pool_n <= kMaxPoolIns) {
         // Own items first: all but the tail from the LDS counter, the tail
         // through this instruction's cursor; then the group's leftovers.  No
@@ -833,11 +914,6 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     return true;
 }
 
-// Byte offset in the dynamic LDS of the 8 KiB (1 KiB per wave) that the
-// opcode-6 cache warming writes into: after the SiLU staging area.
-__device__ __forceinline__ uint32_t lds_prefetch_offset(const KParams &p) {
-    return (uint32_t)p.F * 4u;
-}
 
 // ---------------------------------------------------------------------------
 // opcode 6: ExpertDownProjFused  (python_vm.py:284-314)
@@ -1147,29 +1223,6 @@ __device__ __forceinline__ void matvec_rows(SharedState &sh, const uint16_t *mat
     }
 }
 
-// The first item of a wave in matvec_rows (rows r0 + 2 * wave and the next),
-// first min(nc, 8) chunks, loaded ahead: issued before a wait on inputs that
-// the weights do not depend on, so the weight stream overlaps the wait.
-constexpr int kAheadChunks = 8;
-struct PairAhead {
-    u32x4 a[kAheadChunks], b[kAheadChunks];
-};
-
-__device__ __forceinline__ void pair_ahead_load(PairAhead &r, const uint16_t *mat, size_t ld, int col0, int nc,
-                                                int r0, int nrows) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (2 * wave >= nrows) return;
-    const int ra = r0 + 2 * wave;
-    const u32x4 *wa = reinterpret_cast<const u32x4 *>(mat + (size_t)ra * ld + col0) + lane;
-    const u32x4 *wb = reinterpret_cast<const u32x4 *>(mat + (size_t)(ra + 1) * ld + col0) + lane;
-#pragma unroll
-    for (int i = 0; i < kAheadChunks; ++i)
-        if (i < nc) {
-            r.a[i] = load_stream(wa + i * 64);
-            r.b[i] = load_stream(wb + i * 64);
-        }
-}
-
 // matvec_rows whose first item per wave was loaded by pair_ahead_load with
 // the same arguments.
 template <typename Fn>
@@ -1309,8 +1362,6 @@ constexpr int kKvChunkBytes = 16384;
 constexpr int kKvRingMax = 8;
 constexpr int kAttnSub = 4;  // ring slots scored per softmax rescale
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void global_void_t;
 
 __device__ __forceinline__ void stage_kv(unsigned char *dst, const uint16_t *kbase, const uint16_t *vbase,
                                          uint32_t row_bytes, int t, int dp) {
@@ -1949,7 +2000,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         bool ok = true;
         switch (op) {
         case 0: break;
-        case 5: ok = op_rms_router_upgate<kE>(p, sh, act, ins, c, tim); break;
+        case 5: ok = op_rms_router_upgate<kE, kAttn>(p, sh, act, ins, c, tim); break;
         case 6: ok = op_expert_downproj(p, sh, act, ins, c, tim); break;
         case 8: ok = op_predict<kE>(p, sh, act, ins, c, tim); break;
         case 1:

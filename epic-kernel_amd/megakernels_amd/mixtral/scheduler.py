@@ -265,13 +265,17 @@ def schedule_lm_head(globs: MixtralGlobals):
 # DAGs
 # ---------------------------------------------------------------------------
 
-def make_dag(globs: MixtralGlobals, stop_after_op: str | None = None, layer_limit: int | None = None):
-    """Whole-model DAG with the reference's node order and dependencies."""
+def make_dag(globs: MixtralGlobals, stop_after_op: str | None = None, layer_limit: int | None = None,
+             predict: bool = True):
+    """Whole-model DAG with the reference's node order and dependencies.
+    ``predict=False`` leaves out opcode 8 (the speculative expert
+    prediction), which also turns off the early expert-weight loads that
+    consume it: the "predictor disabled" side of BASELINE config 5."""
     nodes: list[DAG_Node] = []
     layers = layer_limit if layer_limit is not None else globs.num_hidden_layers
     last: list[DAG_Node] = []
     for layer in range(layers):
-        new, last = make_dag_layer(globs, layer, last, stop_after_op)
+        new, last = make_dag_layer(globs, layer, last, stop_after_op, predict)
         nodes.extend(new)
     if layers == globs.num_hidden_layers and stop_after_op is None:
         head = [DAG_Node(ins, last) for ins in schedule_lm_head(globs)]
@@ -280,7 +284,8 @@ def make_dag(globs: MixtralGlobals, stop_after_op: str | None = None, layer_limi
     return nodes, DAG_Node(NoOp(), last)
 
 
-def make_dag_layer(globs: MixtralGlobals, layer_idx: int, prev_layer_outputs, stop_after_op: str | None = None):
+def make_dag_layer(globs: MixtralGlobals, layer_idx: int, prev_layer_outputs, stop_after_op: str | None = None,
+                   predict: bool = True):
     parts = pick_num_attention_partitions(globs.pos_id + 1, 0, globs.num_kv_heads, globs.sm_count(),
                                           getattr(globs, "attn_partition_policy", "reference"),
                                           globs.attn_kv_block_size)
@@ -293,7 +298,8 @@ def make_dag_layer(globs: MixtralGlobals, layer_idx: int, prev_layer_outputs, st
         for b in n.instruction.block_indices():
             by_block[b] = n
     nodes.extend(qkv_nodes)
-    nodes.extend(DAG_Node(ins, prev_layer_outputs) for ins in schedule_speculative_predict(globs, layer_idx))
+    if predict:
+        nodes.extend(DAG_Node(ins, prev_layer_outputs) for ins in schedule_speculative_predict(globs, layer_idx))
     if stop_after_op == "qkv":
         return nodes, qkv_nodes
 

@@ -10,7 +10,10 @@ convention (``include/util.cuh:220-252``):
 * 46       own items done (work sharing; opcode 2: wave 0's positions)
 * 47       instruction's stores complete and arrival made
 * 48       first weight load issued
-* 49       first staged data in place (opcode 2: its K/V ring has landed)
+* 49       first staged data in place (opcode 2: its K/V ring has landed;
+           opcode 5: speculative expert loads issued)
+* 50       opcode 5 of a whole-model launch: predicted and selected experts
+           (bytes p0, p1, s0, s1; 0xff = no prediction), not a time
 
 This module turns that record into what the reference's plotting scripts
 derive from theirs, as numbers rather than figures:
@@ -269,6 +272,37 @@ def phase_summary(rec: TimingRecord, percentiles=(0, 10, 50, 90, 100)) -> dict:
     return out
 
 
+T_PREDICTION = 50
+
+
+def prediction_agreement(rec: TimingRecord):
+    """Opcode 8's prediction against opcode 5's selection, from the first
+    opcode-5 instruction of each layer (every workgroup routes identically):
+    (layers with a prediction, top-1 agreement, top-2 set agreement), or None
+    when no layer had one."""
+    ins = rec.instructions
+    seen = {}
+    W, Q = ins.shape[:2]
+    for w in range(W):
+        for q in range(Q):
+            if int(ins[w, q, 0]) != 5 or rec.dense:
+                continue
+            layer = int(ins[w, q, 1])
+            if layer in seen:
+                continue
+            v = int(rec.timings[w, q, T_PREDICTION]) & 0xFFFFFFFF
+            p0, p1, s0, s1 = v & 0xFF, (v >> 8) & 0xFF, (v >> 16) & 0xFF, (v >> 24) & 0xFF
+            if p0 == 0xFF or v == 0:
+                continue
+            seen[layer] = (p0, p1, s0, s1)
+    if not seen:
+        return None
+    n = len(seen)
+    top1 = sum(p0 == s0 for p0, _, s0, _ in seen.values()) / n
+    top2 = sum({p0, p1} == {s0, s1} for p0, p1, s0, s1 in seen.values()) / n
+    return n, top1, top2
+
+
 def stage_windows(rec: TimingRecord) -> dict:
     """Per (layer, opcode): (first start, last end, last completion) in us --
     the critical-path view of a whole-model step (the LM head is layer -1)."""
@@ -314,6 +348,10 @@ def format_report(rec: TimingRecord, peak_gbs: float = 8000.0) -> str:
         ends = [max(b for (lay, _), (_, b, _) in win.items() if lay == L) for L in layers]
         if len(ends) > 2:
             lines.append(f"mean layer period {np.mean(np.diff(ends)):.1f} us over {len(layers)} layers")
+    agree = prediction_agreement(rec)
+    if agree is not None:
+        n, top1, top2 = agree
+        lines.append(f"expert prediction over {n} layers: top-1 agreement {top1:.1%}, top-2 set agreement {top2:.1%}")
     lines.append("event percentiles (us): p0 p10 p50 p90 p100")
     for (name, ev), v in phase_summary(rec).items():
         lines.append(f"  {name:26s} {ev:10s} " + " ".join(f"{x:7.1f}" for x in v))

@@ -103,7 +103,11 @@ enum {
     MK_TEVENT_AT_GMEM_STORE = 46,
     MK_TEVENT_DONE_GMEM_STORE = 47,
     MK_TEVENT_FIRST_LOAD = 48,
-    MK_TEVENT_FIRST_USE = 49
+    MK_TEVENT_FIRST_USE = 49,
+    /* opcode 5 of a whole-model launch: the experts opcode 8 predicted and
+     * the ones selected, one byte each (predicted 0, 1, selected 0, 1 from
+     * the low byte up; 0xff = no prediction) -- not a time */
+    MK_TEVENT_PREDICTION = 50
 };
 
 typedef struct mk_mixtral_globals {

@@ -141,3 +141,24 @@ def test_dense_vm_byte_model_covers_each_weight_once():
     assert by_op[1] == L * (c.num_attention_heads + 2 * c.num_key_value_heads) * D * H * 2
     assert by_op[4] == L * H * c.num_attention_heads * D * 2
     assert by_op[2] == L * c.num_key_value_heads * 41 * 2 * D * 2
+
+
+def test_prediction_agreement_from_the_record():
+    """Slot 50 of each layer's first opcode-5 instruction holds the predicted
+    and selected experts (bytes p0, p1, s0, s1)."""
+    from megakernels_amd.trace import prediction_agreement
+
+    W, Q = 1, 6
+    ins = np.zeros((W, Q, 32), dtype=np.int32)
+    tim = np.zeros((W, Q, 128), dtype=np.int32)
+    packs = [(3, 5, 3, 5), (3, 5, 5, 3), (1, 2, 1, 7), (0xFF, 0xFF, 2, 4)]
+    for q, (p0, p1, s0, s1) in enumerate(packs):
+        ins[0, q, :4] = [5, q, 0, 4]
+        tim[0, q, 50] = np.uint32(p0 | p1 << 8 | s0 << 16 | s1 << 24).view(np.int32)
+    ins[0, 4, :4] = [5, 0, 4, 4]  # a second instruction of layer 0: ignored
+    tim[0, 4, 50] = np.uint32(1 | 2 << 8 | 6 << 16 | 7 << 24).view(np.int32)
+    rec = TimingRecord(tim, ins, H, F, E, 8, 16)
+    n, top1, top2 = prediction_agreement(rec)
+    assert n == 3  # the layer without a prediction is left out
+    assert top1 == pytest.approx(2 / 3) and top2 == pytest.approx(2 / 3)
+    assert "top-2 set agreement 66.7%" in format_report(rec)
