@@ -281,7 +281,10 @@ def decode_bench(args):
                                        prefill=prefill, predictor_sigma=args.predict_sigma)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
-    gen = MK_Generator.build(model, prefill, mode=args.assign,
+    gkw = {"attention_partitions": args.partitions}
+    if args.qkv_block:
+        gkw["qkv_block_size"] = args.qkv_block
+    gen = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                              dag_kwargs=None if llama else {"predict": not args.no_predict})
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
@@ -332,6 +335,8 @@ def decode_bench(args):
             "predictor_sigma": args.predict_sigma,
             "predictor": None if llama else not args.no_predict,
             "assignment": args.assign,
+            "qkv_block_size": g.qkv_block_size,
+            "partition_policy": args.partitions,
         },
         "roofline": {
             "bound": "hbm",
@@ -418,6 +423,10 @@ def main():
                     help="timed decode steps (default: 256 for c3, 128 for c4/c5, as BASELINE states them)")
     ap.add_argument("--assign", default="rr", choices=["rr", "zz", "wave", "dag"],
                     help="c3/c4/c5: instruction-to-worker assignment of the whole-model schedule")
+    ap.add_argument("--qkv-block", type=int, default=0,
+                    help="c3/c4/c5: QKV row block size (default: picked for the worker count)")
+    ap.add_argument("--partitions", default="mi355x", choices=["mi355x", "reference"],
+                    help="c3/c4/c5: split-KV partition policy")
     ap.add_argument("--no-predict", action="store_true",
                     help="c4/c5: leave opcode 8 (expert prediction) and the early expert loads that use it out")
     ap.add_argument("--predict-sigma", type=float, default=None,

@@ -158,7 +158,7 @@ struct AttnParams {
     int32_t qkv_bs, kv_bs, lm_bs, lm_red;
     float attn_scale;
     int32_t skip_red;
-    int32_t kv_ring;  // opcode-2 LDS ring chunks (1 .. kKvRingMax)
+    int32_t kv_ring;  // opcode-2 LDS ring chunks (kAttnSub or kKvRingMax)
 };
 
 // Per-workgroup state that outlives a single instruction.
@@ -1405,16 +1405,19 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
     const uint16_t *kbase = a.kc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
     const uint16_t *vbase = a.vc + (size_t)layer * a.T * a.Hkv * D + (size_t)kv * D;
     const uint32_t row_bytes = (uint32_t)(a.Hkv * D * 2);
-    auto stage_round = [&](int r) {
-        for (int k = 0; k < nb; ++k) {
-            const int ch = r * nb + k;
-            if (ch >= nch) break;
+    // Chunk ch lives in ring slot ch % nb.  Groups of kAttnSub chunks are
+    // computed in order; with an 8-chunk ring two groups are resident, and
+    // a consumed group's slots are restaged with the group two later while
+    // the next group is computed.
+    auto stage_chunks = [&](int c0, int c1) {
+        for (int ch = c0; ch < c1 && ch < nch; ++ch) {
             const int t = first + ch * CT;
-            stage_kv(wave_lds + k * kKvChunkBytes, kbase, vbase, row_bytes, (t < t1 && t != pos) ? t : t0, dp);
+            stage_kv(wave_lds + (ch % nb) * kKvChunkBytes, kbase, vbase, row_bytes, (t < t1 && t != pos) ? t : t0,
+                     dp);
         }
     };
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    stage_round(0);
+    stage_chunks(0, nb);
 
     // producers: the GQA query heads, the key head and the value head
     const int bph = D / a.qkv_bs;
@@ -1432,6 +1435,14 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
 #pragma unroll
         for (int j = 0; j < 8; ++j) q[h][j] *= qscale;
     }
+    // the new position's rows, device-coherent: loaded now, patched over the
+    // row t0 staged in their place once their chunk has landed
+    u32x4 kn = {0u, 0u, 0u, 0u}, vn = {0u, 0u, 0u, 0u};
+    if (own_new) {
+        const uint32_t off = (uint32_t)pos * row_bytes + (uint32_t)dp * 16u;
+        kn = ld_dev128(kbase, off);
+        vn = ld_dev128(vbase, off);
+    }
     float M[GQA], L[GQA], acc[GQA][8];
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
@@ -1440,79 +1451,86 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
     }
-    const int rounds = (nch + nb - 1) / nb;
-    for (int r = 0; r < rounds; ++r) {
-        if (r > 0) stage_round(r);
-        // the new position's rows, device-coherent, patched over the row t0
-        // that was staged in their place
-        const bool patch = own_new && c_new / nb == r;  // uniform
-        u32x4 kn = {0u, 0u, 0u, 0u}, vn = {0u, 0u, 0u, 0u};
-        if (patch) {
-            const uint32_t off = (uint32_t)pos * row_bytes + (uint32_t)dp * 16u;
-            kn = ld_dev128(kbase, off);
-            vn = ld_dev128(vbase, off);
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging has landed in LDS
-        if (r == 0) stamp(tim, MK_TEVENT_FIRST_USE);
-        if (patch && first + c_new * CT == pos) {
-            const int k = c_new - r * nb;
-            kl[k * (kKvChunkBytes / 16)] = kn;
-            kl[k * (kKvChunkBytes / 16) + kKvChunkBytes / 32] = vn;
-        }
-        for (int k0 = 0; k0 < nb; k0 += kAttnSub) {
-            // scores of ring slots k0 .. k0 + kAttnSub
-            float sc[GQA][kAttnSub];
-#pragma unroll
-            for (int u = 0; u < kAttnSub; ++u) {
-                const int k = k0 + u, ch = r * nb + k;
-                const bool live = k < nb && ch < nch;  // uniform
-                const bool valid = live && first + ch * CT < t1;
-                float kf[8];
-                if (live) widen8(kl[k * (kKvChunkBytes / 16)], kf);
-#pragma unroll
-                for (int h = 0; h < GQA; ++h) {
-                    float d = 0.f;
-                    if (live) {
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) d = fmaf(q[h][j], kf[j], d);
-                        d = group_sum(d, G);
-                    }
-                    sc[h][u] = valid ? d : -INFINITY;
-                }
+    const bool two = nb >= 2 * kAttnSub;  // two groups resident (uniform)
+    const int ngroups = (nch + kAttnSub - 1) / kAttnSub;
+    for (int g = 0; g < ngroups; ++g) {
+        const int cg = g * kAttnSub;
+        if (g == 0) {
+            __builtin_amdgcn_s_waitcnt(0);  // the first ring (and the new rows) landed
+            stamp(tim, MK_TEVENT_FIRST_USE);
+        } else if (two) {
+            // everything but the next group's loads (2 per chunk) has landed
+            const int next = min(max(nch - cg - kAttnSub, 0), kAttnSub);
+            switch (next) {
+            case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+            case 1: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+            case 2: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+            case 3: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+            default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
             }
-            // rescale the slot's running state once, to the new max
-            float ref[GQA];
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        if (own_new && c_new >= cg && c_new < cg + kAttnSub && first + c_new * CT == pos) {
+            kl[(c_new % nb) * (kKvChunkBytes / 16)] = kn;
+            kl[(c_new % nb) * (kKvChunkBytes / 16) + kKvChunkBytes / 32] = vn;
+        }
+        // scores of the group's chunks
+        float sc[GQA][kAttnSub];
+#pragma unroll
+        for (int u = 0; u < kAttnSub; ++u) {
+            const int ch = cg + u, k = ch % nb;
+            const bool live = ch < nch;  // uniform
+            const bool valid = live && first + ch * CT < t1;
+            float kf[8];
+            if (live) widen8(kl[k * (kKvChunkBytes / 16)], kf);
 #pragma unroll
             for (int h = 0; h < GQA; ++h) {
-                float mb = M[h];
+                float d = 0.f;
+                if (live) {
 #pragma unroll
-                for (int u = 0; u < kAttnSub; ++u) mb = fmaxf(mb, sc[h][u]);
-                ref[h] = mb == -INFINITY ? 0.f : mb;
-                const float alpha = exp2_fast(M[h] - ref[h]);  // 0 while M is -inf, 1 if the max holds
-                L[h] *= alpha;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] *= alpha;
-                M[h] = mb;
-            }
-#pragma unroll
-            for (int u = 0; u < kAttnSub; ++u) {
-                const int k = k0 + u, ch = r * nb + k;
-                if (!(k < nb && ch < nch)) continue;  // uniform
-                // rows staged for masked positions may hold anything
-                // (the row pos_id is read before this launch writes it)
-                const u32x4 vraw = first + ch * CT < t1 ? kl[k * (kKvChunkBytes / 16) + kKvChunkBytes / 32]
-                                                        : u32x4{0u, 0u, 0u, 0u};
-                float vf[8];
-                widen8(vraw, vf);
-#pragma unroll
-                for (int h = 0; h < GQA; ++h) {
-                    const float pr = exp2_fast(sc[h][u] - ref[h]);  // 0 for masked positions
-                    L[h] += pr;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pr, vf[j], acc[h][j]);
+                    for (int j = 0; j < 8; ++j) d = fmaf(q[h][j], kf[j], d);
+                    d = group_sum(d, G);
                 }
+                sc[h][u] = valid ? d : -INFINITY;
             }
         }
+        // rescale the slot's running state once, to the new max
+        float ref[GQA];
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+            float mb = M[h];
+#pragma unroll
+            for (int u = 0; u < kAttnSub; ++u) mb = fmaxf(mb, sc[h][u]);
+            ref[h] = mb == -INFINITY ? 0.f : mb;
+            const float alpha = exp2_fast(M[h] - ref[h]);  // 0 while M is -inf, 1 if the max holds
+            L[h] *= alpha;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] *= alpha;
+            M[h] = mb;
+        }
+#pragma unroll
+        for (int u = 0; u < kAttnSub; ++u) {
+            const int ch = cg + u, k = ch % nb;
+            if (ch >= nch) continue;  // uniform
+            // rows staged for masked positions may hold anything
+            // (the row pos_id is read before this launch writes it)
+            const u32x4 vraw = first + ch * CT < t1 ? kl[k * (kKvChunkBytes / 16) + kKvChunkBytes / 32]
+                                                    : u32x4{0u, 0u, 0u, 0u};
+            float vf[8];
+            widen8(vraw, vf);
+#pragma unroll
+            for (int h = 0; h < GQA; ++h) {
+                const float pr = exp2_fast(sc[h][u] - ref[h]);  // 0 for masked positions
+                L[h] += pr;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pr, vf[j], acc[h][j]);
+            }
+        }
+        // this group's slots are free (its LDS reads fed the sums above):
+        // restage them with the group that maps onto them
+        const int cn = cg + (two ? 2 : 1) * kAttnSub;
+        if (cn < nch) stage_chunks(cn, cn + kAttnSub);
     }
 
     stamp(tim, MK_TEVENT_AT_GMEM_STORE);  // wave 0's positions done
@@ -2218,10 +2236,11 @@ size_t lds_bytes_for(const mk_mixtral_globals *g, int kv_ring) {
     return need > (size_t)kMinLdsBytes ? need : (size_t)kMinLdsBytes;
 }
 
-// Largest opcode-2 ring (chunks, <= kKvRingMax) whose launch fits in
-// `max_lds` bytes of LDS per workgroup; 0 if even one chunk does not.
+// Largest opcode-2 ring (chunks: kKvRingMax or kAttnSub) whose launch fits
+// in `max_lds` bytes of LDS per workgroup; 0 if neither does.
 int kv_ring_for(const mk_mixtral_globals *g, size_t max_lds) {
-    for (int nb = kKvRingMax; nb >= 1; --nb)
+    // whole groups of kAttnSub chunks (opcode 2 computes a group at a time)
+    for (int nb = kKvRingMax; nb >= kAttnSub; nb -= kAttnSub)
         if (lds_bytes_for(g, nb) + sizeof(SharedState) <= max_lds) return nb;
     return 0;
 }
@@ -2302,7 +2321,7 @@ size_t lds_bytes_llama(const mk_llama_globals *g, int kv_ring) {
 }
 
 int kv_ring_llama(const mk_llama_globals *g, size_t max_lds) {
-    for (int nb = kKvRingMax; nb >= 1; --nb)
+    for (int nb = kKvRingMax; nb >= kAttnSub; nb -= kAttnSub)
         if (lds_bytes_llama(g, nb) + sizeof(SharedState) <= max_lds) return nb;
     return 0;
 }

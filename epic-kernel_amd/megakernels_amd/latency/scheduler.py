@@ -11,6 +11,12 @@ Counterpart of ``megakernels/demos/latency/scheduler.py:1-440``:
   down-projection (column chunk, row block) jobs split over workers so that
   each instruction stays within one column chunk.
 * ``make_dag`` builds the per-layer DAG of ``:267-428``.
+* ``qkv_block_size`` is picked for the worker count among 16 and 8 rows
+  (``pick_block_size``: at 3B and 256 workers, 8-row blocks give every
+  worker at most 24 QKV rows where the reference's 16-row blocks leave 32 on
+  some and 16 on others; 4-row blocks measured slower), and the
+  split-KV partition count follows the MI355X policy of the Mixtral
+  scheduler; ``attention_partitions="reference"`` restores the reference's.
 
 The reference asserts more than one block per worker in every partitioner
 (it targets 132-160 SMs and 1B/3B shapes); here a partitioner with fewer
@@ -27,7 +33,7 @@ import torch
 from ..instructions import NoOp
 from ..scheduler import DAG_Node, ScheduleBuilder
 from ..utils import assert_div, get_sm_count
-from ..mixtral.scheduler import pick_num_attention_partitions
+from ..mixtral.scheduler import pick_block_size, pick_num_attention_partitions
 from .instructions import (
     AttentionReduction,
     DownProjResidual,
@@ -44,7 +50,8 @@ BARRIER_OPS = 10
 
 
 def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 0,
-                 sm_count: int | None = None, attention_partitions: str = "mi355x") -> Globals:
+                 sm_count: int | None = None, attention_partitions: str = "mi355x",
+                 qkv_block_size: int | None = None) -> Globals:
     """Activation buffers plus ``model``'s stacked weights (duck-typed like
     the reference's ``LlamaForCausalLM``); ``sm_count`` overrides the device
     query (needed when the globals live on the CPU); ``attention_partitions``
@@ -103,7 +110,8 @@ def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 
         o_proj_block_size=16,
         lm_head_block_size=16,
         matvec_reduction_size=math.gcd(cfg.intermediate_size, cfg.hidden_size),
-        qkv_block_size=16,
+        qkv_block_size=qkv_block_size or pick_block_size((Hq + 2 * Hkv) * D, workers,
+                                                         tuple(b for b in (16, 8) if D % b == 0)),
         attn_kv_block_size=16,
         attn_reduction_size=Hq // Hkv,
     )

@@ -35,14 +35,16 @@ class MK_Generator:
 
     @classmethod
     def build(cls, model, prompt_len: int, mode: str = "rr", sm_count: int | None = None, dag_kwargs=None,
-              **launch_kwargs):
+              globals_kwargs=None, **launch_kwargs):
         """Globals for ``model`` with the KV cache filled up to ``prompt_len``
         positions, the whole-model schedule assigned with ``mode``, and a
         generator over it.  The model type picks the VM: a model with
         ``stacked_params.expert_gate`` is Mixtral, one with
         ``stacked_params.gate_proj`` the dense Llama VM
         (``megakernels/dispatch.py`` maps model types the same way).
-        ``dag_kwargs`` go to the VM's ``make_dag`` (e.g. ``predict=False``)."""
+        ``dag_kwargs`` go to the VM's ``make_dag`` (e.g. ``predict=False``),
+        ``globals_kwargs`` to its ``make_globals`` (block sizes, partition
+        policy)."""
         if hasattr(model.stacked_params, "gate_proj"):
             from ..latency.mk import LatencyMK_Interpreter
             from ..latency.scheduler import make_dag as dag_fn
@@ -51,7 +53,7 @@ class MK_Generator:
             interpreter = LatencyMK_Interpreter()
         else:
             dag_fn, globals_fn, interpreter = make_dag, make_globals, MixtralMK_Interpreter()
-        globs = globals_fn(model, seq_len=prompt_len, sm_count=sm_count)
+        globs = globals_fn(model, seq_len=prompt_len, sm_count=sm_count, **(globals_kwargs or {}))
         globs.pos_id = prompt_len
         nodes, end = dag_fn(globs, **(dag_kwargs or {}))
         schedule = Schedule(globs, nodes, end)

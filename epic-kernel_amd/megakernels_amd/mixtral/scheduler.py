@@ -27,6 +27,10 @@ Differences, all MI355X-motivated and recorded here:
   most 160 / kv_heads): the kernel's partial attention is VALU-bound per
   workgroup, so more, shorter partitions finish sooner.
   ``attention_partitions="reference"`` reproduces the reference partition.
+* ``qkv_block_size`` is picked the same way among 16 and 8 rows (at config
+  4 and 256 workers, 8-row blocks give every worker 24 QKV rows where 16-row
+  blocks leave 32 on half of them; 4-row blocks measured slower); it stays a
+  divisor of head_dim.
 * ``make_moe_dag`` builds the MoE-only slice of one layer (optional opcode 8,
   then opcode 5 and opcode 6) for running the hot path in isolation; the
   attention prefix it skips is represented by pre-filling the O-proj barrier
@@ -116,6 +120,7 @@ def make_globals(
     expert_proj_block_size: int | None = None,
     down_proj_block_size: int | None = None,
     attention_partitions: str = "mi355x",
+    qkv_block_size: int | None = None,
 ) -> MixtralGlobals:
     """Allocate activation buffers and wrap ``model``'s stacked weights.
 
@@ -204,7 +209,9 @@ def make_globals(
         o_proj_block_size=16,
         lm_head_block_size=16,
         matvec_reduction_size=math.gcd(F, H),
-        qkv_block_size=16,
+        qkv_block_size=qkv_block_size or pick_block_size(
+            (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * head_dim, workers,
+            tuple(b for b in (16, 8) if head_dim % b == 0)),
         attn_kv_block_size=16,
         attn_reduction_size=cfg.num_attention_heads // cfg.num_key_value_heads,
         router_bias=getattr(sp, "router_bias", None),

@@ -43,6 +43,19 @@ def test_stage_attention(prefill):
     _check(case, f"attention prefill {prefill}", keys=("k_new", "v_new", "q", "attn_out"))
 
 
+@pytest.mark.parametrize("config,workers", [(TINY, 16), (SMALL, 8)])
+def test_stage_attention_long_partitions(config, workers):
+    """Few workers and a long context: hundreds of positions per partition,
+    so the K/V ring is restaged group after group while earlier groups are
+    computed (head dim 128 and 64)."""
+    case = FullCase(with_layers(config, 1), seed=9, prefill=3000, stop_after_op="reduction", layer_limit=1,
+                    workers=workers)
+    parts = max(i.num_partials for i in case.linear if i.opcode() == 2)
+    assert (3001 / parts) / (8 * 64 // (case.g_gpu.head_dim // 8)) > 8  # more chunks than the ring holds
+    case.step(13)
+    _check(case, f"attention long partitions {config.hidden_size}", keys=("k_new", "v_new", "q", "attn_out"))
+
+
 def test_stage_oproj():
     case = FullCase(with_layers(SMALL, 1), seed=3, prefill=300, stop_after_op="oproj", layer_limit=1)
     case.step(11)
