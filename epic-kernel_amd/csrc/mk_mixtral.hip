@@ -69,7 +69,7 @@
 // N growing from 1 to MK_SPIN_SLEEP_MAX, so hundreds of idle workgroups do not
 // keep the counter's memory channel busy while others still stream weights.
 #ifndef MK_SPIN_SLEEP_MAX
-#define MK_SPIN_SLEEP_MAX 16
+#define MK_SPIN_SLEEP_MAX 4
 #endif
 #ifndef MK_CLAIM_LOOKAHEAD
 #define MK_CLAIM_LOOKAHEAD 1
