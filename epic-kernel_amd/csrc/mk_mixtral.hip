@@ -1006,6 +1006,11 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
         const uint16_t *row = p.down + ((size_t)(layer * p.E + e) * p.H + row0 + d.row) * (size_t)p.F;
         load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane, min(d.n, kEarlyChunks));
     }
+    // The residual rows this instruction updates: when opcode 5 ran here,
+    // the O-projection barrier it waited for has made them final, so they
+    // are read now instead of after the sums (one dependent load less).
+    uint32_t hpre = 0;
+    if (known && tid < first_batch) hpre = ld_dev16(p.hidden + row0 + tid);
 
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     int32_t *ready = bar_at(p, layer, 5);
@@ -1094,7 +1099,7 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
                 d1 += sh.part[(r * 2 + 1) * kMaxSegments + sg];
             }
             uint16_t *hp = p.hidden + row0 + b0 + r;
-            float h = bf2f(ld_dev16(hp));
+            float h = bf2f(known && b0 == 0 ? hpre : ld_dev16(hp));  // r == tid in the first batch
             h = rbf(h + rbf(s0 * rbf(d0)));
             h = rbf(h + rbf(s1 * rbf(d1)));
             st_dev16(hp, f2bf(h));
@@ -1714,19 +1719,34 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     if (threadIdx.x == 0) sh.next_item = kWaves;
     const int K = a.Hq * a.D;  // reduction length
     const uint16_t *wo = a.oproj + (size_t)layer * p.H * K;
+    const int r0 = b0 * p.oproj_bs, nrows = (b1 - b0) * p.oproj_bs;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // The residual rows of each wave's first item are final once the
+    // previous layer's down-projection is complete (or at layer 0): read
+    // them now instead of after the sums (one dependent load less).
+    if (threadIdx.x == 0)
+        sh.flag = layer == 0 || (int)ld_dev32(bar_at(p, layer - 1, 6)) >= p.down_arrivals;
+    __syncthreads();
+    const bool hfinal = sh.flag != 0 && 2 * wave < nrows;  // uniform
+    __syncthreads();
+    const int rpre = r0 + 2 * wave;
+    uint32_t hpair = 0;
+    if (hfinal && lane == 0) hpair = ld_dev32(p.hidden + rpre);
     PairAhead pre;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, b0 * p.oproj_bs, (b1 - b0) * p.oproj_bs);
+    pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, r0, nrows);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(a.attn_out, (uint32_t)v * 16u);
     __syncthreads();
-    matvec_rows_ahead(sh, pre, wo, (size_t)K, 0, K / kChunkElems, act, b0 * p.oproj_bs, (b1 - b0) * p.oproj_bs,
-                      [&](int r, float s) {
-                          uint16_t *hp = p.hidden + r;
-                          st_dev16(hp, f2bf(bf2f(ld_dev16(hp)) + rbf(s)));
-                      });
+    matvec_rows_ahead(sh, pre, wo, (size_t)K, 0, K / kChunkElems, act, r0, nrows, [&](int r, float s) {
+        uint16_t *hp = p.hidden + r;
+        const uint32_t h = hfinal && r == rpre       ? (hpair & 0xffffu)
+                           : hfinal && r == rpre + 1 ? (hpair >> 16)
+                                                     : ld_dev16(hp);
+        st_dev16(hp, f2bf(bf2f(h) + rbf(s)));
+    });
     drain_and_sync();
     arrive(bar_at(p, layer, 4), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
