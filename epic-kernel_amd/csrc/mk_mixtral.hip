@@ -2274,7 +2274,7 @@ int validate_attention(const mk_mixtral_globals *g) {
         !g->attn_lse_intermediates || !g->attn_out_intermediates || !g->logits)
         return MK_ERR_INVALID_ARGUMENT;
     const int Hq = g->num_attention_heads, Hkv = g->num_kv_heads, D = g->head_dim;
-    if (Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 4 || (Hq / Hkv) & (Hq / Hkv - 1)) return MK_ERR_UNSUPPORTED;
+    if (Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 4) return MK_ERR_UNSUPPORTED;
     if (D != 64 && D != 128) return MK_ERR_UNSUPPORTED;
     if ((Hq * D) % kChunkElems) return MK_ERR_UNSUPPORTED;
     if (g->qkv_block_size < 2 || g->qkv_block_size % 2 || D % g->qkv_block_size) return MK_ERR_INVALID_ARGUMENT;

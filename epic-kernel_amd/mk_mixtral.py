@@ -436,7 +436,7 @@ def _attention_shape(qkv, attn_ln, o_proj, lm_norm, lm_head, k_cache, v_cache, r
     _check_tensor("attn_lse_intermediates", lse_int, torch.float32, dev)
     _check(lse_int.dim() == 2, "attn_lse_intermediates must be [Hq, P]")
     Hq, P = lse_int.shape
-    _check(Hkv > 0 and Hq % Hkv == 0 and Hq // Hkv in (1, 2, 4), f"need Hq / Hkv in (1, 2, 4), got {Hq} / {Hkv}")
+    _check(Hkv > 0 and Hq % Hkv == 0 and 1 <= Hq // Hkv <= 4, f"need Hq / Hkv in 1..4, got {Hq} / {Hkv}")
     QKV = (Hq + 2 * Hkv) * D
     _check_tensor("qkv_weights", qkv, bf16, dev, (L, QKV, H))
     _check_tensor("attn_norm_weights", attn_ln, bf16, dev, (L, H))

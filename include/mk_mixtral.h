@@ -182,7 +182,7 @@ typedef struct mk_mixtral_globals {
     int32_t lm_head_block_size;    /* logit rows per LM-head block (16)      */
     int32_t lm_head_reduction;     /* columns per LM-head reduction block (2048) */
     int32_t num_attention_heads;   /* Hq                                     */
-    int32_t num_kv_heads;          /* Hkv; Hq / Hkv in {1, 2, 4}             */
+    int32_t num_kv_heads;          /* Hkv; Hq / Hkv in 1..4                  */
     int32_t head_dim;              /* D: 64 or 128                           */
     int32_t vocab_size;            /* V                                      */
     int32_t kv_capacity;           /* T: positions per layer in the KV cache */
