@@ -285,7 +285,8 @@ def decode_bench(args):
     if args.qkv_block:
         gkw["qkv_block_size"] = args.qkv_block
     gen = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
-                             dag_kwargs=None if llama else {"predict": not args.no_predict})
+                             dag_kwargs=None if llama else {"predict": not args.no_predict},
+                             device_argmax=not args.host_argmax)
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
@@ -337,6 +338,7 @@ def decode_bench(args):
             "assignment": args.assign,
             "qkv_block_size": g.qkv_block_size,
             "partition_policy": args.partitions,
+            "argmax": "torch, between launches" if args.host_argmax else "in-kernel, with the next embedding",
         },
         "roofline": {
             "bound": "hbm",
@@ -431,6 +433,9 @@ def main():
                     help="c4/c5: leave opcode 8 (expert prediction) and the early expert loads that use it out")
     ap.add_argument("--predict-sigma", type=float, default=None,
                     help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
+    ap.add_argument("--host-argmax", action="store_true",
+                    help="c3/c4/c5: torch.argmax and the embedding lookup between launches, as the reference's "
+                         "generator (default: inside the launch)")
     ap.add_argument("--no-skewed", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))

@@ -147,6 +147,11 @@ struct KParams {
     // 2 * H / down_bs; dense Llama: (F / red_cols) * (H / down_bs))
     int32_t down_arrivals;
     int32_t red_cols;  // dense down-projection column chunk (matvec_reduction_size)
+    // decode-driver extension (NULL: off): the last workgroup to exit writes
+    // argmax(logits) to argmax_out and, with next_embed, copies that row of
+    // the embedding table into hidden (the next step's input)
+    int64_t *argmax_out;
+    const uint16_t *next_embed;
 };
 
 struct AttnParams {
@@ -2005,6 +2010,86 @@ __device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &
 // Exit protocol: the last workgroup out (failed or not) zeroes the
 // work-sharing counters for the next launch.  Every other workgroup has
 // finished all of its scratch accesses before it increments the counter.
+// Running argmax in torch.argmax's order: NaN above every number, then the
+// larger value, then the lower index (idx < 0: empty).
+struct ArgBest {
+    float v;
+    int idx;
+    bool nan;
+};
+
+__device__ __forceinline__ bool arg_better(const ArgBest &b, const ArgBest &a) {
+    if (b.idx < 0) return false;
+    if (a.idx < 0) return true;
+    if (a.nan || b.nan) return a.nan && b.nan ? b.idx < a.idx : b.nan;
+    return b.v > a.v || (b.v == a.v && b.idx < a.idx);
+}
+
+__device__ __forceinline__ void arg_take(ArgBest &a, float v, int idx) {
+    const ArgBest b{v, idx, v != v};
+    if (arg_better(b, a)) a = b;
+}
+
+// Decode-driver tail of a launch, run by the last workgroup to exit (every
+// LM-head instruction has completed by then): argmax over the V logits,
+// written to p.argmax_out, and with p.next_embed the embedding row of that
+// token copied into hidden.  Replaces the generator's torch.argmax and
+// embedding lookup between launches (megakernels/generators.py:121-145).
+__device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
+    const AttnParams &a = *p.ap;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int V = a.V, nv = V >> 3;
+    ArgBest best{0.f, -1, false};
+    // 16 B per lane, four loads in flight per thread
+    for (int base = 0; base < nv; base += 4 * kThreads) {
+        u32x4 x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int v = base + k * kThreads + tid;
+            x[k] = v < nv ? ld_dev128(a.logits, (uint32_t)v * 16u) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int v = base + k * kThreads + tid;
+            if (v < nv) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    arg_take(best, bf2f(x[k][j] & 0xffffu), 8 * v + 2 * j);
+                    arg_take(best, bf2f(x[k][j] >> 16), 8 * v + 2 * j + 1);
+                }
+            }
+        }
+    }
+    for (int i = 8 * nv + tid; i < V; i += kThreads) arg_take(best, bf2f(ld_dev16(a.logits + i)), i);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const ArgBest o{__shfl_xor(best.v, m), __shfl_xor(best.idx, m), __shfl_xor((int)best.nan, m) != 0};
+        if (arg_better(o, best)) best = o;
+    }
+    if (lane == 0) {
+        sh.red[wave] = best.v;
+        sh.wave_cnt[wave] = best.idx;
+        sh.red_ss[wave] = best.nan ? 1.f : 0.f;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        ArgBest r{0.f, -1, false};
+        for (int w = 0; w < kWaves; ++w) {
+            const ArgBest o{sh.red[w], sh.wave_cnt[w], sh.red_ss[w] != 0.f};
+            if (arg_better(o, r)) r = o;
+        }
+        *p.argmax_out = (int64_t)r.idx;
+        sh.flag = r.idx;
+    }
+    __syncthreads();
+    if (p.next_embed != nullptr) {
+        const int tok = sh.flag;
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(p.next_embed + (size_t)tok * p.H);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(p.hidden);
+        for (int v = tid; v < (p.H >> 3); v += kThreads) dst[v] = src[v];
+    }
+}
+
 __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
     drain_and_sync();
     if (threadIdx.x == 0) {
@@ -2013,6 +2098,7 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
     }
     __syncthreads();
     if (sh.flag) {
+        if (p.argmax_out != nullptr && p.ap != nullptr && !aborted(p)) exit_argmax(p, sh);
         const int n = 2 * (int)gridDim.x * p.queue_len;
         for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
         drain_and_sync();
@@ -2323,6 +2409,11 @@ int validate(const mk_mixtral_globals *g) {
                          g->predictor_weights};
     for (const void *v : vec)
         if (v != nullptr && !aligned16(v)) return MK_ERR_INVALID_ARGUMENT;
+    if (g->next_embed_weights != nullptr && (g->argmax_out == nullptr || !aligned16(g->next_embed_weights)))
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->argmax_out != nullptr &&
+        (g->qkv_weights == nullptr || g->logits == nullptr || (reinterpret_cast<uintptr_t>(g->argmax_out) & 7u)))
+        return MK_ERR_INVALID_ARGUMENT;
     return validate_attention(g);
 }
 
@@ -2390,6 +2481,9 @@ int validate_llama(const mk_llama_globals *g) {
     for (const void *v : vec)
         if (!aligned16(v)) return MK_ERR_INVALID_ARGUMENT;
     if (reinterpret_cast<uintptr_t>(g->logits) & 3u) return MK_ERR_INVALID_ARGUMENT;
+    if (g->next_embed_weights != nullptr && (g->argmax_out == nullptr || !aligned16(g->next_embed_weights)))
+        return MK_ERR_INVALID_ARGUMENT;
+    if (g->argmax_out != nullptr && (reinterpret_cast<uintptr_t>(g->argmax_out) & 7u)) return MK_ERR_INVALID_ARGUMENT;
     return MK_OK;
 }
 
@@ -2442,6 +2536,8 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.work_sharing = 0;
     kp.red_cols = g->matvec_reduction_size;
     kp.down_arrivals = (g->intermediate_size / g->matvec_reduction_size) * (g->hidden_size / g->down_proj_block_size);
+    kp.argmax_out = g->argmax_out;
+    kp.next_embed = g->next_embed_weights;
     kp.attn = 1;
     AttnParams a{};
     a.qkv = g->qkv_weights;
@@ -2571,6 +2667,8 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
+    kp.argmax_out = g->argmax_out;
+    kp.next_embed = g->next_embed_weights;
     kp.attn = g->qkv_weights != nullptr;
     kp.ap = nullptr;
     if (kp.attn) {

@@ -1,11 +1,20 @@
 """Greedy batch-1 decode driver over the persistent kernel.
 
 Counterpart of ``MK_Generator`` (``megakernels/generators.py:95-166``), for
-the Mixtral VM and the dense Llama VM alike: a step embeds the input token into ``hidden_states``, refills the barrier
-tensor, sets ``pos_id``, zeroes the logits (the LM head accumulates its
-column blocks into them), launches the whole-model schedule once, and takes
-the argmax of the logits.  ``generate`` runs steps back to back, feeding each
-output token to the next step, as ``MK_Generator.generate`` does.
+the Mixtral VM and the dense Llama VM alike: a step embeds the input token
+into ``hidden_states``, refills the barrier tensor, sets ``pos_id``, zeroes
+the logits (the Mixtral LM head accumulates its column blocks into them),
+launches the whole-model schedule once, and takes the argmax of the logits.
+``generate`` runs steps back to back, feeding each output token to the next
+step, as ``MK_Generator.generate`` does.
+
+The argmax and the next step's embedding run inside the launch
+(``argmax_out`` / ``next_embed_weights`` of the C ABI): the kernel's last
+workgroup writes the token straight into ``output_tokens`` and copies its
+embedding row into ``hidden_states``, where the reference runs
+``torch.argmax`` and the embedding lookup between launches
+(``megakernels/generators.py:121-145``).  ``device_argmax=False`` restores
+the torch calls.
 
 The schedule is built once (``make_dag`` over all layers plus the LM head)
 and reused for every position; partial-attention instructions cover the
@@ -25,11 +34,12 @@ from .scheduler import make_dag, make_globals
 
 class MK_Generator:
     def __init__(self, model, interpreter: MixtralMK_Interpreter, schedule: Schedule, barrier_fill_val: int = 0,
-                 **launch_kwargs):
+                 device_argmax: bool = True, **launch_kwargs):
         self.model = model
         self.interpreter = interpreter
         self.schedule = schedule
         self.barrier_fill_val = barrier_fill_val
+        self.device_argmax = device_argmax
         self.launch_kwargs = launch_kwargs
         self.fill()
 
@@ -64,22 +74,47 @@ class MK_Generator:
         self.schedule.globs.barriers.fill_(self.barrier_fill_val)
 
     def run(self, input_ids: torch.Tensor, pos_id: int) -> torch.Tensor:
+        """One step from ``input_ids``; returns the output token (0-d)."""
+        return self._step(input_ids, pos_id)
+
+    def _step(self, input_ids, pos_id: int, out: torch.Tensor | None = None, embedded: bool = False,
+              embed_next: bool = False) -> torch.Tensor:
+        """One launch.  ``embedded``: the previous launch already wrote this
+        step's input embedding into ``hidden_states``.  ``out``: a 0-d int64
+        view the kernel writes the token into.  ``embed_next``: the launch
+        also writes that token's embedding into ``hidden_states``."""
         globs = self.schedule.globs
-        globs.hidden_states.copy_(self.model.embed_tokens[input_ids.reshape(-1)[0]])
+        if not embedded:
+            globs.hidden_states.copy_(self.model.embed_tokens[input_ids.reshape(-1)[0]])
         self.fill()
         globs.pos_id = pos_id
         globs.logits.zero_()
-        self.interpreter.interpret(globs, **self.launch_kwargs)
-        return torch.argmax(globs.logits, dim=-1)
+        if not self.device_argmax:
+            self.interpreter.interpret(globs, **self.launch_kwargs)
+            return torch.argmax(globs.logits, dim=-1)
+        if out is None:
+            out = torch.empty((), dtype=torch.long, device=globs.logits.device)
+        self.interpreter.interpret(globs, argmax_out=out,
+                                   next_embed_weights=self.model.embed_tokens if embed_next else None,
+                                   **self.launch_kwargs)
+        return out
 
     def generate(self, output_tokens: torch.Tensor, prompt_len: int, ntok: int, ntok_already_generated: int = 1):
         """Fill ``output_tokens[:, ntok_already_generated : +ntok]`` greedily
-        (``megakernels/generators.py:148-166``)."""
+        (``megakernels/generators.py:148-166``).  With the in-kernel argmax
+        each launch writes its token into ``output_tokens`` and the embedding
+        of that token for the next launch."""
+        chain = (self.device_argmax and output_tokens.dtype == torch.long and output_tokens.shape[0] == 1
+                 and output_tokens.is_contiguous())
         for i in range(ntok):
             input_pos = ntok_already_generated + i - 1
             input_ids = output_tokens[:, input_pos:input_pos + 1]
             pos_id = prompt_len + ntok_already_generated + i - 1
-            output_tokens[:, input_pos + 1] = self.run(input_ids, pos_id=pos_id)
+            if chain:
+                self._step(input_ids, pos_id, out=output_tokens[0, input_pos + 1], embedded=i > 0,
+                           embed_next=i + 1 < ntok)
+            else:
+                output_tokens[:, input_pos + 1] = self.run(input_ids, pos_id=pos_id)
         return output_tokens
 
     def timed_generate(self, first_token: int, prompt_len: int, ntok: int, warmup: int = 2):

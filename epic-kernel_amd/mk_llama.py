@@ -12,8 +12,9 @@ under the reference's 3B module name.
 
 Keyword-only additions (defaults are the reference's compiled-in values):
 the block sizes and ``matvec_reduction_size`` the instructions were built
-with, ``spin_timeout_us``, ``record_timings`` and ``debug_sync`` (as in
-``mk_mixtral``).  There is no fallback.
+with, ``spin_timeout_us``, ``record_timings``, ``argmax_out`` /
+``next_embed_weights`` and ``debug_sync`` (as in ``mk_mixtral``).  There is
+no fallback.
 """
 
 from __future__ import annotations
@@ -27,7 +28,7 @@ from mk_mixtral import MKError, _check, _check_tensor, _error_text, raise_if_fai
 
 __all__ = ["mk_llama", "mk_llama_3b", "MkLlamaGlobals", "build_llama_struct"]
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _P = ctypes.c_void_p
 
 
@@ -88,6 +89,8 @@ class MkLlamaGlobals(ctypes.Structure):
         ("status", _P),
         ("spin_timeout_us", ctypes.c_uint32),
         ("record_timings", ctypes.c_int32),
+        ("argmax_out", ctypes.c_void_p),
+        ("next_embed_weights", ctypes.c_void_p),
     ]
 
 
@@ -129,6 +132,8 @@ def build_llama_struct(
     status=None,
     spin_timeout_us: int = 0,
     record_timings: bool = False,
+    argmax_out=None,
+    next_embed_weights=None,
 ) -> MkLlamaGlobals:
     """Validate the reference-ordered arguments and fill the C struct;
     ``TypeError``/``ValueError`` before anything reaches the GPU."""
@@ -233,6 +238,7 @@ def build_llama_struct(
     g.status = None if status is None else status.data_ptr()
     g.spin_timeout_us = int(spin_timeout_us)
     g.record_timings = int(bool(record_timings))
+    g.argmax_out, g.next_embed_weights = mk_mixtral._decode_tail(argmax_out, next_embed_weights, True, dev, H)
     return g
 
 

@@ -25,6 +25,12 @@ sizes are the compile-time 16):
     other workers' opcode-5 instructions (default off: each instruction
     processes exactly its own rows; results and barrier counts are the same
     either way);
+``argmax_out`` / ``next_embed_weights``
+    decode-driver extension (whole-model launches): the launch ends by
+    writing ``argmax(logits)`` (torch.argmax's first-maximum, NaN-maximal
+    order) into the int64 ``argmax_out``, and with the ``[V, H]`` embedding
+    table sets ``hidden_states`` to that token's row, the next step's input
+    -- what the reference's generator does with torch between launches;
 ``debug_sync``
     synchronise after the launch and raise :class:`MKDeviceError` if the
     kernel recorded a failure.
@@ -54,7 +60,7 @@ __all__ = [
 _HERE = Path(__file__).resolve().parent
 _LIB_NAME = "libmk_mixtral.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 STATUS_WORDS = 16
 MAX_EXPERTS = 16
 
@@ -158,6 +164,8 @@ class MkMixtralGlobals(ctypes.Structure):
         ("spin_timeout_us", ctypes.c_uint32),
         ("record_timings", ctypes.c_int32),
         ("work_sharing", ctypes.c_int32),
+        ("argmax_out", _P),
+        ("next_embed_weights", _P),
     ]
 
 
@@ -308,6 +316,8 @@ def build_globals_struct(
     spin_timeout_us: int = 0,
     record_timings: bool = False,
     work_sharing: bool = False,
+    argmax_out=None,
+    next_embed_weights=None,
 ) -> MkMixtralGlobals:
     """Validate the reference-ordered arguments and fill the C struct.
 
@@ -419,7 +429,23 @@ def build_globals_struct(
     g.spin_timeout_us = int(spin_timeout_us)
     g.record_timings = int(bool(record_timings))
     g.work_sharing = int(bool(work_sharing))
+    g.argmax_out, g.next_embed_weights = _decode_tail(argmax_out, next_embed_weights, attn is not None, dev, H)
     return g
+
+
+def _decode_tail(argmax_out, next_embed_weights, has_lm_head: bool, dev, H: int):
+    """Pointers of the optional in-kernel argmax / next-token embedding."""
+    if next_embed_weights is not None:
+        _check(argmax_out is not None, "next_embed_weights needs argmax_out")
+        _check_tensor("next_embed_weights", next_embed_weights, torch.bfloat16, dev)
+        _check(next_embed_weights.dim() == 2 and next_embed_weights.shape[1] == H,
+               f"next_embed_weights must be [V, {H}]")
+    if argmax_out is None:
+        return None, None
+    _check(has_lm_head, "argmax_out needs the LM head (attention tensors)")
+    _check(isinstance(argmax_out, torch.Tensor) and argmax_out.dtype == torch.int64 and argmax_out.device == dev
+           and argmax_out.numel() >= 1, "argmax_out must be an int64 tensor on the launch device", TypeError)
+    return argmax_out.data_ptr(), None if next_embed_weights is None else next_embed_weights.data_ptr()
 
 
 def _attention_shape(qkv, attn_ln, o_proj, lm_norm, lm_head, k_cache, v_cache, rope_cos, rope_sin, q_rope,

@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define MK_LLAMA_ABI_VERSION 1
+#define MK_LLAMA_ABI_VERSION 2
 
 typedef struct mk_llama_globals {
     uint32_t struct_size;          /* sizeof(mk_llama_globals) */
@@ -117,6 +117,12 @@ typedef struct mk_llama_globals {
     int32_t *status;               /* NULL: the library's per-device status words */
     uint32_t spin_timeout_us;      /* 0 = 2 s */
     int32_t record_timings;
+
+    /* decode-driver extension (no reference counterpart; the reference's
+     * generator runs torch.argmax and the embedding between launches,
+     * megakernels/generators.py:121-145), as in mk_mixtral_globals */
+    int64_t *argmax_out;                /* argmax of logits when the launch ends, or NULL */
+    const uint16_t *next_embed_weights; /* [V, H] bf16 or NULL: hidden_states := row *argmax_out */
 } mk_llama_globals;
 
 /* Launch one decode step of the dense VM.  Returns MK_OK or an

@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define MK_MIXTRAL_ABI_VERSION 2
+#define MK_MIXTRAL_ABI_VERSION 3
 #define MK_INTS_PER_INSTRUCTION 32
 #define MK_TIMING_SLOTS 128
 #define MK_STATUS_WORDS 16
@@ -201,6 +201,17 @@ typedef struct mk_mixtral_globals {
                                       unclaimed rows of other opcode-5
                                       instructions of the same layer (same
                                       results, same barrier counts) */
+
+    /* decode-driver extension, no counterpart in the reference kernel: its
+     * generator takes torch.argmax of the logits and embeds the token between
+     * launches (megakernels/generators.py:121-145).  NULL keeps the reference
+     * semantics; both need the LM head (attention tensors present). */
+    int64_t *argmax_out;           /* when the launch ends: argmax of logits, the
+                                      first maximal index (NaN counts as
+                                      maximal, as in torch.argmax) */
+    const uint16_t *next_embed_weights; /* [V, H] bf16, needs argmax_out: when
+                                      the launch ends, hidden_states := row
+                                      *argmax_out (the next step's input) */
 } mk_mixtral_globals;
 
 /* Launch one persistent-kernel pass over the instruction queues.

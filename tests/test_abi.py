@@ -100,6 +100,24 @@ def test_llama_launch_validation_needs_no_gpu(lib):
         mk_llama.build_llama_struct(*args, 0, 1.0, 1e-5, False)
 
 
+def test_decode_tail_arguments_are_checked():
+    """argmax_out / next_embed_weights: int64 output, an LM head to take the
+    argmax of, and the embedding table only together with argmax_out."""
+    out = torch.zeros((), dtype=torch.int64)
+    emb = torch.zeros(8, 512, dtype=torch.bfloat16)
+    dev = torch.device("cpu")
+    assert mk_mixtral._decode_tail(None, None, False, dev, 512) == (None, None)
+    assert mk_mixtral._decode_tail(out, emb, True, dev, 512) == (out.data_ptr(), emb.data_ptr())
+    with pytest.raises(ValueError, match="needs argmax_out"):
+        mk_mixtral._decode_tail(None, emb, True, dev, 512)
+    with pytest.raises(ValueError, match="LM head"):
+        mk_mixtral._decode_tail(out, None, False, dev, 512)
+    with pytest.raises(TypeError):
+        mk_mixtral._decode_tail(out.int(), None, True, dev, 512)
+    with pytest.raises(ValueError, match=r"\[V, 1024\]"):
+        mk_mixtral._decode_tail(out, emb, True, dev, 1024)
+
+
 def test_struct_layout_matches_header(tmp_path):
     fields = [f for f, _ in mk_mixtral.MkMixtralGlobals._fields_]
     src = tmp_path / "layout.c"

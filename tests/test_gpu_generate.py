@@ -32,13 +32,16 @@ def _oracle_generate(model, prompt_len, first, ntok, sm_count):
     return toks, g
 
 
-@pytest.mark.parametrize("prompt_len", [40, 300])
-def test_greedy_tokens_match_oracle(prompt_len):
+@pytest.mark.parametrize("prompt_len,device_argmax", [(40, True), (300, True), (40, False)])
+def test_greedy_tokens_match_oracle(prompt_len, device_argmax):
+    """device_argmax: the launch writes each token into ``tokens`` and the
+    next input's embedding (the default); False: torch.argmax and the
+    embedding lookup between launches, as the reference's generator."""
     ntok = 4
     cpu = make_synthetic_mixtral(TINY, "cpu", 21, full=True, kv_positions=prompt_len + ntok + 1,
                                  prefill=prompt_len, ln_weight_std=0.1)
     gpu = to_device(cpu, "cuda")
-    gen = MK_Generator.build(gpu, prompt_len, debug_sync=True)
+    gen = MK_Generator.build(gpu, prompt_len, device_argmax=device_argmax, debug_sync=True)
     W = gen.schedule.globs.sm_count()
     tokens = torch.zeros(1, ntok + 1, dtype=torch.long, device="cuda")
     tokens[0, 0] = 7
