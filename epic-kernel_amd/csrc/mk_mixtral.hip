@@ -1758,9 +1758,95 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     return true;
 }
 
+// ---- LM-head row items ------------------------------------------------------
+
+// Rows [row, row + nv) (nv <= NR) x NC chunks of 512 columns from col0 into
+// registers, 16 B per lane per chunk.
+template <int NR, int NC>
+__device__ __forceinline__ void load_rows_upto(u32x4 (&w)[NR][NC], const uint16_t *mat, size_t ld, int row, int nv,
+                                               int col0, int lane) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+        if (i < nv) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                w[i][c] = load_stream(reinterpret_cast<const u32x4 *>(mat + (size_t)(row + i) * ld + col0) + c * 64 +
+                                      lane);
+        }
+}
+
+// Matvec of rows [r0, r0 + nrows) (an even count) over NC chunks from col0
+// with the LDS vector x, in items of NR rows (NR * NC loads per lane in
+// flight; a row pair of 512-column chunks keeps too few loads in flight when
+// the rows are short).  `w` holds the wave's first item (item `wave`),
+// loaded by the caller before its wait; later items come from the
+// workgroup's LDS counter.  fn(row, sum_row, sum_row_plus_1) per row pair,
+// called by lane 0.
+template <int NR, int NC, typename Fn>
+__device__ __forceinline__ void rows_matvec(SharedState &sh, u32x4 (&w)[NR][NC], const uint16_t *mat, size_t ld,
+                                            int col0, const u32x4 *x, int r0, int nrows, Fn fn) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nitems = (nrows + NR - 1) / NR;
+    for (int it = wave; it < nitems; it = next_local_item(sh, lane)) {
+        const int row = r0 + it * NR, nv = min(NR, nrows - it * NR);  // even, uniform
+        if (it != wave) load_rows_upto<NR, NC>(w, mat, ld, row, nv, col0, lane);
+        float acc[NR];
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            acc[i] = 0.f;
+            if (i < nv) {
+#pragma unroll
+                for (int k = 0; k < NC; ++k) acc[i] = dot8(w[i][k], x[k * 64 + lane], acc[i]);
+                acc[i] = wave_sum(acc[i]);
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < NR; i += 2)
+                if (i < nv) fn(row + i, acc[i], acc[i + 1]);
+        }
+    }
+}
+
+// NR for NC chunks per row: about 16-24 loads per lane per item.
+template <int NC>
+struct LmRows {
+    static constexpr int kNR = NC <= 2 ? 8 : NC <= 6 ? 4 : 2;
+};
+
 // ---- opcode 7: Mixtral_RMS_LM_Head  (python_vm.py:321-345) ----------------
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// logits[r] += bf16(W[r, cols] . normed[cols]) for a pair of rows at a time:
+// one packed bf16 atomic add per pair (rows are even-aligned).
+__device__ __forceinline__ void lm_atomic_pair(uint16_t *logits, int r, float sa, float sb) {
+    const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(sa)), __builtin_bit_cast(__bf16, (uint16_t)f2bf(sb))};
+    __builtin_amdgcn_global_atomic_fadd_v2bf16((__attribute__((address_space(1))) bf16x2_t *)(logits + r), v);
+}
+
+// The instruction's rows in items of LmRows<NC> rows, the first item of
+// each wave loaded before the wait (the weights do not depend on it).
+template <int NC>
+__device__ __forceinline__ bool lm_head_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+                                             int32_t *tim, int r0, int nrows, int col0) {
+    const AttnParams &a = *p.ap;
+    const int last = p.num_layers - 1;
+    constexpr int NR = LmRows<NC>::kNR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    u32x4 w[NR][NC];
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    if (wave * NR < nrows) load_rows_upto<NR, NC>(w, a.lm_head, (size_t)p.H, r0 + wave * NR, min(NR, nrows - wave * NR), col0, lane);
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    rms_to_lds(p, sh, act, a.lm_norm);
+    rows_matvec<NR, NC>(sh, w, a.lm_head, (size_t)p.H, col0, act + (col0 >> 3), r0, nrows,
+                        [&](int r, float sa, float sb) { lm_atomic_pair(a.logits, r, sa, sb); });
+    drain_and_sync();
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
 
 __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
                            int32_t *tim) {
@@ -1775,16 +1861,22 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    const int col0 = red * a.lm_red;
+    const int r0 = b0 * a.lm_bs, nrows = (b1 - b0) * a.lm_bs;
+    switch (a.lm_red / kChunkElems) {
+    case 1: return lm_head_rows<1>(p, sh, act, c, tim, r0, nrows, col0);
+    case 2: return lm_head_rows<2>(p, sh, act, c, tim, r0, nrows, col0);
+    case 3: return lm_head_rows<3>(p, sh, act, c, tim, r0, nrows, col0);
+    case 4: return lm_head_rows<4>(p, sh, act, c, tim, r0, nrows, col0);
+    default: break;
+    }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.lm_norm);
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    // logits[r] += bf16(W[r, cols] . normed[cols]) for a pair of rows at a
-    // time: one packed bf16 atomic add per pair (rows are even-aligned)
-    const int col0 = red * a.lm_red;
+    // longer reduction blocks: a row pair per item
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = b0 * a.lm_bs, nrows = (b1 - b0) * a.lm_bs;
     for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
         const int ra = r0 + 2 * it;
         float aa = 0.f, ab = 0.f;
@@ -1792,11 +1884,7 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
                  act + (col0 >> 3), a.lm_red / kChunkElems, lane, aa, ab);
         aa = wave_sum(aa);
         ab = wave_sum(ab);
-        if (lane == 0) {
-            const bf16x2_t v = {__builtin_bit_cast(__bf16, (uint16_t)f2bf(aa)), __builtin_bit_cast(__bf16, (uint16_t)f2bf(ab))};
-            __builtin_amdgcn_global_atomic_fadd_v2bf16(
-                (__attribute__((address_space(1))) bf16x2_t *)(a.logits + ra), v);
-        }
+        if (lane == 0) lm_atomic_pair(a.logits, ra, aa, ab);
     }
     drain_and_sync();
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
@@ -1973,7 +2061,30 @@ __device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh,
 
 // Opcode 7, RMS_LM_Head [7, start, end]: RMSNorm with the LM-head norm, then
 // logits[r] = bf16(W[r] . normed) over all hidden columns for rows
-// [start, end) * lm_head_block_size (stored, not accumulated).
+// [start, end) * lm_head_block_size, stored (not accumulated) with one
+// 32-bit coherent store per row pair.
+template <int NC>
+__device__ __forceinline__ bool dense_lm_head_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+                                                   int32_t *tim, int r0, int nrows) {
+    const AttnParams &a = *p.ap;
+    const int last = p.num_layers - 1;
+    constexpr int NR = LmRows<NC>::kNR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    u32x4 w[NR][NC];
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    if (wave * NR < nrows) load_rows_upto<NR, NC>(w, a.lm_head, (size_t)p.H, r0 + wave * NR, min(NR, nrows - wave * NR), 0, lane);
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    rms_to_lds(p, sh, act, a.lm_norm);
+    rows_matvec<NR, NC>(sh, w, a.lm_head, (size_t)p.H, 0, act, r0, nrows, [&](int r, float sa, float sb) {
+        st_dev32(a.logits + r, f2bf(sa) | (f2bf(sb) << 16));
+    });
+    drain_and_sync();
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
 __device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
                                                  const Ctx &c, int32_t *tim) {
     const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
@@ -1986,13 +2097,23 @@ __device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    const int r0 = b0 * a.lm_bs, nrows = (b1 - b0) * a.lm_bs;
+    switch (p.H / kChunkElems) {
+    case 2: return dense_lm_head_rows<2>(p, sh, act, c, tim, r0, nrows);
+    case 3: return dense_lm_head_rows<3>(p, sh, act, c, tim, r0, nrows);
+    case 4: return dense_lm_head_rows<4>(p, sh, act, c, tim, r0, nrows);
+    case 5: return dense_lm_head_rows<5>(p, sh, act, c, tim, r0, nrows);
+    case 6: return dense_lm_head_rows<6>(p, sh, act, c, tim, r0, nrows);
+    case 8: return dense_lm_head_rows<8>(p, sh, act, c, tim, r0, nrows);
+    default: break;
+    }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.lm_norm);
     stamp(tim, MK_TEVENT_FIRST_LOAD);
+    // other hidden sizes: a row pair per item
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = b0 * a.lm_bs, nrows = (b1 - b0) * a.lm_bs;
     for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
         const int ra = r0 + 2 * it;
         float aa = 0.f, ab = 0.f;
@@ -2007,9 +2128,6 @@ __device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &
     return true;
 }
 
-// Exit protocol: the last workgroup out (failed or not) zeroes the
-// work-sharing counters for the next launch.  Every other workgroup has
-// finished all of its scratch accesses before it increments the counter.
 // Running argmax in torch.argmax's order: NaN above every number, then the
 // larger value, then the lower index (idx < 0: empty).
 struct ArgBest {
@@ -2090,6 +2208,10 @@ __device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
     }
 }
 
+// Exit protocol: the last workgroup out (failed or not) zeroes the
+// work-sharing counters for the next launch, after the decode-driver tail
+// when one was asked for.  Every other workgroup has finished all of its
+// scratch accesses before it increments the counter.
 __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
     drain_and_sync();
     if (threadIdx.x == 0) {
