@@ -38,6 +38,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <stddef.h>
@@ -85,6 +86,12 @@
 #define MK_SPEC_ITEMS 1
 #endif
 
+// Dense VM: at most this many opcode-5 items (gate and up rows) staged in LDS
+// by the preceding opcode 4 (fewer when the LDS left over holds fewer).
+#ifndef MK_STAGE_ITEMS
+#define MK_STAGE_ITEMS 16
+#endif
+
 namespace {
 
 constexpr int kThreads = MK_THREADS;
@@ -107,6 +114,11 @@ constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 
 static_assert(kThreads % 64 == 0 && kThreads <= 1024, "wave64 workgroup");
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Instruction words are read through the constant address space: the kernel
+// never writes them, so uniform reads become scalar loads, which wait on
+// their own counter instead of queueing behind the wave's outstanding
+// weight loads (a vector load of an instruction word waits for all of them).
+typedef const __attribute__((address_space(4))) int32_t ins_t;
 typedef __attribute__((address_space(3))) void lds_void_t;          // LDS pointer (global_load_lds destination)
 typedef const __attribute__((address_space(1))) void global_void_t;  // global pointer (global_load_lds source)
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -152,6 +164,10 @@ struct KParams {
     // the embedding table into hidden (the next step's input)
     int64_t *argmax_out;
     const uint16_t *next_embed;
+    // dense VM: opcode-5 items (gate and up rows) that opcode 4 stages in LDS
+    // while it waits, and where (u32x4 index into the dynamic LDS); 0: off
+    int32_t stage_items;
+    int32_t stage_off16;
 };
 
 struct AttnParams {
@@ -183,6 +199,9 @@ struct SharedState {
     int wave_cnt[kWaves];
     int pool_slot[kMaxPoolIns], pool_row0[kMaxPoolIns], pool_nrows[kMaxPoolIns];
     int spec_e[2];  // opcode 5: experts opcode 8 predicted for the layer (-1: none yet)
+    // dense VM: queue slot whose first stage_n opcode-5 items opcode 4 staged
+    // in LDS (-1: none)
+    int stage_slot, stage_n;
 };
 
 struct Ctx {
@@ -782,7 +801,7 @@ __device__ __forceinline__ void steal_upgate(const KParams &p, const SharedState
 }
 
 template <int kE, bool kSpec>
-__device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                                      const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -982,7 +1001,7 @@ __device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 
     return acc;
 }
 
-__device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                    const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1123,7 +1142,7 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
 // ---------------------------------------------------------------------------
 
 template <int kE>
-__device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     if (layer < 0 || layer >= p.num_layers) {
@@ -1275,7 +1294,7 @@ __device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhe
 
 // ---- opcode 1: Mixtral_QKV  (python_vm.py:61-118) -------------------------
 
-__device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                        int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1612,7 +1631,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams 
     return true;
 }
 
-__device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                                 int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int kv = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1635,7 +1654,7 @@ __device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &s
 
 // ---- opcode 3: Mixtral_AttnReduction  (python_vm.py:166-189) --------------
 
-__device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState &sh, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState &sh, ins_t *ins, const Ctx &c,
                                   int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int hs = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1709,7 +1728,51 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
 
 // ---- opcode 4: Mixtral_OProj  (python_vm.py:196-215) ----------------------
 
-__device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+// Dense VM: the first items (gate and up rows, in item order) of an
+// opcode-5 instruction `nx` of `layer` (queue slot `slot`) -- weights that
+// depend on nothing -- streamed into LDS with global_load_lds while the
+// workgroup waits anyway: by opcode 4 for its next instruction while it
+// waits for the attention reduction, else by opcode 5 itself before its own
+// wait.  Opcode 5 then starts on them the moment its wait ends.  Layout:
+// item i, matrix j (0 gate, 1 up), chunk c is the 1 KiB at u32x4 index
+// stage_off16 + ((2 i + j) nc + c) 64, lane order.  The loads complete
+// before the workgroup passes its next barrier.
+__device__ __forceinline__ void stage_dense_upgate(const KParams &p, SharedState &sh, u32x4 *act,
+                                                   ins_t *nx, int slot, int layer) {
+    if (p.stage_items <= 0 || slot >= p.queue_len) return;
+    const int op = __builtin_amdgcn_readfirstlane(nx[0]);
+    const int l = __builtin_amdgcn_readfirstlane(nx[1]);
+    const int n = __builtin_amdgcn_readfirstlane(nx[2]);
+    if (op != 5 || l != layer || n < 1 || n > MK_INTS_PER_INSTRUCTION - 3) return;
+    const int S = min(p.stage_items, n * p.expert_bs);
+    const int nblocks = p.F / p.expert_bs;
+    for (int k = 0; k * p.expert_bs < S; ++k) {
+        const int b = __builtin_amdgcn_readfirstlane(nx[3 + k]);
+        if (b < 0 || b >= nblocks) return;  // opcode 5 reports it
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nc = p.H / kChunkElems;
+    for (int it = wave; it < S; it += kWaves) {
+        const int k = it / p.expert_bs;
+        const int row = __builtin_amdgcn_readfirstlane(nx[3 + k]) * p.expert_bs + it - k * p.expert_bs;
+        const size_t off = ((size_t)layer * p.F + row) * (size_t)p.H;
+        const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
+        const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
+        for (int ch = 0; ch < nc; ++ch) {
+            __builtin_amdgcn_global_load_lds((global_void_t *)(wg + ch * 64),
+                                             (lds_void_t *)(act + p.stage_off16 + ((2 * it) * nc + ch) * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_t *)(wu + ch * 64),
+                                             (lds_void_t *)(act + p.stage_off16 + ((2 * it + 1) * nc + ch) * 64), 16,
+                                             0, 0);
+        }
+    }
+    if (threadIdx.x == 0) {
+        sh.stage_slot = slot;
+        sh.stage_n = S;
+    }
+}
+
+__device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                          int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1740,6 +1803,7 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     PairAhead pre;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, r0, nrows);
+    stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
@@ -1848,7 +1912,7 @@ __device__ __forceinline__ bool lm_head_rows(const KParams &p, SharedState &sh, 
     return true;
 }
 
-__device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1908,7 +1972,7 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
 // silu_out[r] = bf16(bf16(silu(bf16 g)) * bf16 u), g and u the gate and up
 // rows dotted with the normed vector; one arrival per block on [l][4][0].
 // The dense weights are the one-expert case of the opcode-5 item.
-__device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                                 const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int n = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1922,33 +1986,59 @@ __device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &s
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 5, layer, n, nblocks);
         return false;
     }
-    if (threadIdx.x == 0) sh.next_item = kWaves;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int items = n * p.expert_bs, nc = p.H / kChunkElems;
-    // each wave's first item (its gate and up rows) is loaded before the
-    // wait: the weights do not depend on it
-    PairAhead pre;
-    stamp(tim, MK_TEVENT_FIRST_LOAD);
-    if (wave < items) {
-        const int k = wave / p.expert_bs;
-        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + wave - k * p.expert_bs;
-        const size_t off = ((size_t)layer * p.F + row) * (size_t)p.H;
-        const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
-        const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
-#pragma unroll
-        for (int i = 0; i < kAheadChunks; ++i)
-            if (i < nc) {
-                pre.a[i] = load_stream(wg + i * 64);
-                pre.b[i] = load_stream(wu + i * 64);
-            }
+    // items [0, S) staged in LDS: by the preceding opcode 4, else here
+    const bool pre_staged = __builtin_amdgcn_readfirstlane(sh.stage_slot) == c.slot;
+    if (!pre_staged) {
+        stage_dense_upgate(p, sh, act, ins, c.slot, layer);
+        __syncthreads();
     }
+    const int S = __builtin_amdgcn_readfirstlane(sh.stage_slot == c.slot ? sh.stage_n : 0);
+    if (threadIdx.x == 0) sh.next_item = S + kWaves;
+    // each wave's first item from HBM (its gate and up rows) is loaded
+    // before the wait: the weights do not depend on it (issued after the
+    // wait instead, to stream while the staged items are computed, it
+    // measured 7 % slower per decode step)
+    const int ia = S + wave;
+    PairAhead pre;
+    auto load_ahead = [&]() {
+        if (ia < items) {
+            const int k = ia / p.expert_bs;
+            const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + ia - k * p.expert_bs;
+            const size_t off = ((size_t)layer * p.F + row) * (size_t)p.H;
+            const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
+            const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
+#pragma unroll
+            for (int i = 0; i < kAheadChunks; ++i)
+                if (i < nc) {
+                    pre.a[i] = load_stream(wg + i * 64);
+                    pre.b[i] = load_stream(wu + i * 64);
+                }
+        }
+    };
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    load_ahead();
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    if (threadIdx.x == 0) sh.stage_slot = -1;  // every thread has read it (the wait ends in barriers)
     rms_to_lds(p, sh, act, p.ffn_ln + (size_t)layer * p.H);
-    if (wave < items) {  // the item loaded ahead
-        const int k = wave / p.expert_bs;
-        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + wave - k * p.expert_bs;
+    for (int it = wave; it < S; it += kWaves) {  // the staged items
+        const int k = it / p.expert_bs;
+        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + it - k * p.expert_bs;
+        const u32x4 *sg = act + p.stage_off16 + (2 * it) * nc * 64 + lane;
+        const u32x4 *su = sg + nc * 64;
+        float ag = 0.f, au = 0.f;
+        for (int ch = 0; ch < nc; ++ch) {
+            ag = dot8(sg[ch * 64], act[ch * 64 + lane], ag);
+            au = dot8(su[ch * 64], act[ch * 64 + lane], au);
+        }
+        silu_store(p, 0, row, wave_sum(ag), wave_sum(au), lane);
+    }
+    if (ia < items) {  // the item loaded ahead
+        const int k = ia / p.expert_bs;
+        const int row = __builtin_amdgcn_readfirstlane(ins[3 + k]) * p.expert_bs + ia - k * p.expert_bs;
         float ag = 0.f, au = 0.f;
 #pragma unroll
         for (int i = 0; i < kAheadChunks; ++i)
@@ -2037,7 +2127,7 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
     return true;
 }
 
-__device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                               const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2085,7 +2175,7 @@ __device__ __forceinline__ bool dense_lm_head_rows(const KParams &p, SharedState
     return true;
 }
 
-__device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &sh, u32x4 *act, const int32_t *ins,
+__device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                                  const Ctx &c, int32_t *tim) {
     const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2232,13 +2322,16 @@ template <int kE, bool kAttn>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
-    if (threadIdx.x == 0) sh.route_layer = -1;
+    if (threadIdx.x == 0) {
+        sh.route_layer = -1;
+        sh.stage_slot = -1;
+    }
     __syncthreads();
 
     const int w = blockIdx.x;
     for (int q = 0; q < p.queue_len; ++q) {
         const size_t slot = (size_t)w * p.queue_len + q;
-        const int32_t *ins = p.instructions + slot * MK_INTS_PER_INSTRUCTION;
+        ins_t *ins = (ins_t *)(p.instructions) + slot * MK_INTS_PER_INSTRUCTION;
         int32_t *tim = p.timings != nullptr ? p.timings + slot * MK_TIMING_SLOTS : nullptr;
         const int op = __builtin_amdgcn_readfirstlane(ins[0]);
         const Ctx c{w, q};
@@ -2282,13 +2375,16 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
 __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
-    if (threadIdx.x == 0) sh.route_layer = -1;
+    if (threadIdx.x == 0) {
+        sh.route_layer = -1;
+        sh.stage_slot = -1;
+    }
     __syncthreads();
 
     const int w = blockIdx.x;
     for (int q = 0; q < p.queue_len; ++q) {
         const size_t slot = (size_t)w * p.queue_len + q;
-        const int32_t *ins = p.instructions + slot * MK_INTS_PER_INSTRUCTION;
+        ins_t *ins = (ins_t *)(p.instructions) + slot * MK_INTS_PER_INSTRUCTION;
         int32_t *tim = p.timings != nullptr ? p.timings + slot * MK_TIMING_SLOTS : nullptr;
         const int op = __builtin_amdgcn_readfirstlane(ins[0]);
         const Ctx c{w, q};
@@ -2626,7 +2722,16 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     if (rc != MK_OK) return rc;
     const int kv_ring = kv_ring_llama(g, (size_t)st->max_lds);
     if (kv_ring < 1) return MK_ERR_UNSUPPORTED;
-    const size_t lds = lds_bytes_llama(g, kv_ring);
+    size_t lds = lds_bytes_llama(g, kv_ring);
+    // opcode-5 staging area: after the O-proj input and the normed hidden
+    // state (both at offset 0), up to the LDS a workgroup may have
+    const size_t stage_off = ((std::max((size_t)g->hidden_size, (size_t)g->num_attention_heads * g->head_dim) * 2 +
+                               1023) / 1024) * 1024;
+    const size_t stage_item = (size_t)g->hidden_size * 4;
+    const size_t lds_cap = (size_t)st->max_lds - sizeof(SharedState);
+    const size_t stage_items =
+        lds_cap > stage_off ? std::min((size_t)MK_STAGE_ITEMS, (lds_cap - stage_off) / stage_item) : 0;
+    if (stage_items > 0) lds = std::max(lds, stage_off + stage_items * stage_item);
     rc = ensure_scratch(st, kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len);
     if (rc != MK_OK) return rc;
 
@@ -2657,6 +2762,8 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.scratch = st->scratch;
     kp.work_sharing = 0;
     kp.red_cols = g->matvec_reduction_size;
+    kp.stage_items = (int32_t)stage_items;
+    kp.stage_off16 = (int32_t)(stage_off / 16);
     kp.down_arrivals = (g->intermediate_size / g->matvec_reduction_size) * (g->hidden_size / g->down_proj_block_size);
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
@@ -2789,6 +2896,8 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
+    kp.stage_items = 0;
+    kp.stage_off16 = 0;
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
     kp.attn = g->qkv_weights != nullptr;
