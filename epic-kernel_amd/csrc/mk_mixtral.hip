@@ -2725,8 +2725,8 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     size_t lds = lds_bytes_llama(g, kv_ring);
     // opcode-5 staging area: after the O-proj input and the normed hidden
     // state (both at offset 0), up to the LDS a workgroup may have
-    const size_t stage_off = ((std::max((size_t)g->hidden_size, (size_t)g->num_attention_heads * g->head_dim) * 2 +
-                               1023) / 1024) * 1024;
+    const size_t at0 = std::max((size_t)g->hidden_size, (size_t)g->num_attention_heads * g->head_dim);
+    const size_t stage_off = ((at0 * 2 + 1023) / 1024) * 1024;
     const size_t stage_item = (size_t)g->hidden_size * 4;
     const size_t lds_cap = (size_t)st->max_lds - sizeof(SharedState);
     const size_t stage_items =
