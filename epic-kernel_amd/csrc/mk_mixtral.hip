@@ -182,6 +182,13 @@ struct AttnParams {
     int32_t kv_ring;  // opcode-2 LDS ring chunks (kAttnSub or kKvRingMax)
 };
 
+// The attention parameters are read through the constant address space,
+// like the instruction words: the host writes them before the launch and the
+// kernel never does, so the reads are scalar loads (cached, and not queued
+// behind the wave's outstanding weight loads as vector loads would be).
+typedef const __attribute__((address_space(4))) AttnParams attn_c;
+__device__ __forceinline__ attn_c &attn_of(const KParams &p) { return *(attn_c *)(p.ap); }
+
 // Per-workgroup state that outlives a single instruction.
 struct SharedState {
     float red[kWaves * MK_MAX_EXPERTS];
@@ -1300,7 +1307,7 @@ __device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
     if (!need_attention(p, c, 1, layer)) return false;
-    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    attn_c &a = attn_of(p);  // valid: attention tensors are present
     const int D = a.D, qkv_rows = (a.Hq + 2 * a.Hkv) * D;
     if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * a.qkv_bs > qkv_rows) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 1, layer, b0, b1);
@@ -1409,7 +1416,7 @@ __device__ __forceinline__ void stage_kv(unsigned char *dst, const uint16_t *kba
 // Scores are kept in log2 units (q pre-scaled by attn_scale * log2(e)), so
 // exp(s) = exp2(s2) and the partition's LSE is log2(L) + M.
 template <int GQA>
-__device__ __forceinline__ bool partial_attn(const KParams &p, const AttnParams &a, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, SharedState &sh, u32x4 *act, const Ctx &c,
                              int layer, int kv, int nparts, int pidx, int32_t *tim) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int D = a.D, G = D / 8, TPW = 64 / G, CT = kWaves * TPW;
@@ -1638,7 +1645,7 @@ __device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &s
     const int nparts = __builtin_amdgcn_readfirstlane(ins[3]);
     const int pidx = __builtin_amdgcn_readfirstlane(ins[4]);
     if (!need_attention(p, c, 2, layer)) return false;
-    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    attn_c &a = attn_of(p);  // valid: attention tensors are present
     if (layer < 0 || layer >= p.num_layers || kv < 0 || kv >= a.Hkv || nparts < 1 || pidx < 0 || pidx >= nparts ||
         (!a.skip_red && pidx >= a.P)) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 2, layer, kv, pidx);
@@ -1662,7 +1669,7 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
     const int terminal = __builtin_amdgcn_readfirstlane(ins[4]);
     const int n = __builtin_amdgcn_readfirstlane(ins[5]);
     if (!need_attention(p, c, 3, layer)) return false;
-    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    attn_c &a = attn_of(p);  // valid: attention tensors are present
     const int gqa = a.Hq / a.Hkv;
     const int out_slot = (n >= 0 && n <= MK_INTS_PER_INSTRUCTION - 7) ? __builtin_amdgcn_readfirstlane(ins[6 + n]) : -1;
     bool bad = layer < 0 || layer >= p.num_layers || hs < 0 || hs + gqa > a.Hq || n < 1 ||
@@ -1779,7 +1786,7 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     const int b1 = __builtin_amdgcn_readfirstlane(ins[3]);
     const int red = __builtin_amdgcn_readfirstlane(ins[4]);
     if (!need_attention(p, c, 4, layer)) return false;
-    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    attn_c &a = attn_of(p);  // valid: attention tensors are present
     if (layer < 0 || layer >= p.num_layers || b0 < 0 || b1 < b0 || (int64_t)b1 * p.oproj_bs > p.H || red != 0) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 4, layer, b0, b1);
         return false;
@@ -1894,7 +1901,7 @@ __device__ __forceinline__ void lm_atomic_pair(uint16_t *logits, int r, float sa
 template <int NC>
 __device__ __forceinline__ bool lm_head_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                              int32_t *tim, int r0, int nrows, int col0) {
-    const AttnParams &a = *p.ap;
+    attn_c &a = attn_of(p);
     const int last = p.num_layers - 1;
     constexpr int NR = LmRows<NC>::kNR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1919,7 +1926,7 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
     const int red = __builtin_amdgcn_readfirstlane(ins[3]);
     const int last = p.num_layers - 1;
     if (!need_attention(p, c, 7, last)) return false;
-    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    attn_c &a = attn_of(p);  // valid: attention tensors are present
     if (b0 < 0 || b1 < b0 || (int64_t)b1 * a.lm_bs > a.V || red < 0 || (int64_t)(red + 1) * a.lm_red > p.H) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 7, last, b0, b1);
         return false;
@@ -2156,7 +2163,7 @@ __device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh,
 template <int NC>
 __device__ __forceinline__ bool dense_lm_head_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                    int32_t *tim, int r0, int nrows) {
-    const AttnParams &a = *p.ap;
+    attn_c &a = attn_of(p);
     const int last = p.num_layers - 1;
     constexpr int NR = LmRows<NC>::kNR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2181,7 +2188,7 @@ __device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &
     const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
     const int last = p.num_layers - 1;
     if (!need_attention(p, c, 7, last)) return false;
-    const AttnParams &a = *p.ap;  // valid: attention tensors are present
+    attn_c &a = attn_of(p);  // valid: attention tensors are present
     if (b0 < 0 || b1 < b0 || (int64_t)b1 * a.lm_bs > a.V) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 7, last, b0, b1);
         return false;
@@ -2244,7 +2251,7 @@ __device__ __forceinline__ void arg_take(ArgBest &a, float v, int idx) {
 // token copied into hidden.  Replaces the generator's torch.argmax and
 // embedding lookup between launches (megakernels/generators.py:121-145).
 __device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
-    const AttnParams &a = *p.ap;
+    attn_c &a = attn_of(p);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int V = a.V, nv = V >> 3;
     ArgBest best{0.f, -1, false};
