@@ -168,6 +168,7 @@ struct KParams {
     // while it waits, and where (u32x4 index into the dynamic LDS); 0: off
     int32_t stage_items;
     int32_t stage_off16;
+    int32_t lds_bytes;  // dynamic LDS of the launch
 };
 
 struct AttnParams {
@@ -1259,12 +1260,31 @@ __device__ __forceinline__ void matvec_rows(SharedState &sh, const uint16_t *mat
     }
 }
 
+// Row pairs kWaves .. kWaves + nst - 1 of a matvec_rows_ahead (rows r0 + 2 q
+// and the next, nc chunks from column col0) streamed into LDS at `stage`
+// with global_load_lds, each wave its pairs q = kWaves + wave (+ kWaves ..):
+// pair q, row j, chunk c at stage[((2 (q - kWaves) + j) nc + c) 64], lane
+// order.  They land before the workgroup's next barrier.
+__device__ __forceinline__ void stage_pairs(const uint16_t *mat, size_t ld, int col0, int nc, int r0, int nst,
+                                            u32x4 *stage) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int q = wave; q < nst; q += kWaves) {
+        const uint16_t *ra = mat + (size_t)(r0 + 2 * (q + kWaves)) * ld + col0;
+        for (int j = 0; j < 2; ++j)
+            for (int ch = 0; ch < nc; ++ch)
+                __builtin_amdgcn_global_load_lds(
+                    (global_void_t *)(reinterpret_cast<const u32x4 *>(ra + j * ld) + ch * 64 + lane),
+                    (lds_void_t *)(stage + ((2 * q + j) * nc + ch) * 64), 16, 0, 0);
+    }
+}
+
 // matvec_rows whose first item per wave was loaded by pair_ahead_load with
-// the same arguments.
+// the same arguments, and whose pairs kWaves .. kWaves + nst - 1 were staged
+// at `stage` by stage_pairs.
 template <typename Fn>
 __device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhead &pre, const uint16_t *mat,
                                                   size_t ld, int col0, int nc, const u32x4 *x, int r0, int nrows,
-                                                  Fn fn) {
+                                                  Fn fn, const u32x4 *stage = nullptr, int nst = 0) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (2 * wave < nrows) {
         const int ra = r0 + 2 * wave;
@@ -1289,7 +1309,15 @@ __device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhe
     for (int it = next_local_item(sh, lane); 2 * it < nrows; it = next_local_item(sh, lane)) {
         const int ra = r0 + 2 * it;
         float aa = 0.f, ab = 0.f;
-        dot_pair(mat + (size_t)ra * ld + col0, mat + (size_t)(ra + 1) * ld + col0, x, x, nc, lane, aa, ab);
+        if (it - kWaves < nst) {
+            const u32x4 *sa = stage + (2 * (it - kWaves)) * nc * 64 + lane, *sb = sa + nc * 64;
+            for (int ch = 0; ch < nc; ++ch) {
+                aa = dot8(sa[ch * 64], x[lane + ch * 64], aa);
+                ab = dot8(sb[ch * 64], x[lane + ch * 64], ab);
+            }
+        } else {
+            dot_pair(mat + (size_t)ra * ld + col0, mat + (size_t)(ra + 1) * ld + col0, x, x, nc, lane, aa, ab);
+        }
         aa = wave_sum(aa);
         ab = wave_sum(ab);
         if (lane == 0) {
@@ -1318,15 +1346,22 @@ __device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 
     const uint16_t *wq = a.qkv + (size_t)layer * qkv_rows * p.H;
     PairAhead pre;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    pair_ahead_load(pre, wq, (size_t)p.H, 0, p.H / kChunkElems, r0, nrows);
+    const int nc = p.H / kChunkElems;
+    pair_ahead_load(pre, wq, (size_t)p.H, 0, nc, r0, nrows);
+    // the pairs after the ones loaded ahead go to LDS, after the normed
+    // hidden state and the block's outputs, as far as the launch's LDS holds
+    const int soff16 = (((p.H * 2 + nrows * 4) + 1023) / 1024) * 64;  // u32x4 units
+    const int nst = min(max(nrows / 2 - kWaves, 0), max(p.lds_bytes / 16 - soff16, 0) / (2 * nc * 64));
+    stage_pairs(wq, (size_t)p.H, 0, nc, r0, nst, act + soff16);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 1, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.attn_ln + (size_t)layer * p.H);
 
     float *rowv = reinterpret_cast<float *>(act + (p.H >> 3));  // the block's outputs, bf16-rounded
-    matvec_rows_ahead(sh, pre, wq, (size_t)p.H, 0, p.H / kChunkElems, act, r0, nrows,
-                      [&](int r, float s) { rowv[r - r0] = rbf(s); });
+    matvec_rows_ahead(
+        sh, pre, wq, (size_t)p.H, 0, nc, act, r0, nrows, [&](int r, float s) { rowv[r - r0] = rbf(s); },
+        act + soff16, nst);
     __syncthreads();
 
     // RoPE on q and k rows (interleaved pairs (2i, 2i+1) share cos/sin[2i]):
@@ -2771,6 +2806,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.red_cols = g->matvec_reduction_size;
     kp.stage_items = (int32_t)stage_items;
     kp.stage_off16 = (int32_t)(stage_off / 16);
+    kp.lds_bytes = (int32_t)lds;
     kp.down_arrivals = (g->intermediate_size / g->matvec_reduction_size) * (g->hidden_size / g->down_proj_block_size);
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
@@ -2905,6 +2941,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.red_cols = 0;
     kp.stage_items = 0;
     kp.stage_off16 = 0;
+    kp.lds_bytes = (int32_t)lds;
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
     kp.attn = g->qkv_weights != nullptr;
