@@ -427,8 +427,9 @@ def main():
                     help="c3/c4/c5: instruction-to-worker assignment of the whole-model schedule")
     ap.add_argument("--qkv-block", type=int, default=0,
                     help="c3/c4/c5: QKV row block size (default: picked for the worker count)")
-    ap.add_argument("--partitions", default="mi355x", choices=["mi355x", "reference"],
-                    help="c3/c4/c5: split-KV partition policy")
+    ap.add_argument("--partitions", default="mi355x",
+                    help="c3/c4/c5: split-KV partition policy: mi355x, mi355x:N (at most N partitions per KV head) "
+                         "or reference")
     ap.add_argument("--no-predict", action="store_true",
                     help="c4/c5: leave opcode 8 (expert prediction) and the early expert loads that use it out")
     ap.add_argument("--predict-sigma", type=float, default=None,

@@ -22,7 +22,7 @@ Differences, all MI355X-motivated and recorded here:
   Passing ``16`` reproduces the reference partition.  The oracle reads the
   block sizes from the globals, so results do not depend on this choice.
 * the split-KV partition count defaults to the MI355X policy of
-  :func:`pick_num_attention_partitions` (chunks of >= 64 positions, up to 25
+  :func:`pick_num_attention_partitions` (chunks of >= 112 positions, up to 25
   partitions per KV head) instead of the reference's (>= 256 positions, at
   most 160 / kv_heads): the kernel's partial attention is VALU-bound per
   workgroup, so more, shorter partitions finish sooner.
@@ -66,6 +66,10 @@ ATTN_PARTITION_CAP = 160
 #: partials a terminal reduction can list: its 32-word instruction holds 7
 #: other words
 MAX_REDUCTION_LIST = 25
+#: fewest positions per partition of the MI355X policy (swept at config 3:
+#: 17-19 partitions of 112-128 positions beat 22 of 96 by 1.5 %, and 13-15 by
+#: 2 %; configs 4 and 5 stay at the cap)
+MIN_PARTITION_POSITIONS = 112
 
 
 def pick_num_attention_partitions(prompt_len: int, ntok: int, num_kv_heads: int, sm_count: int,
@@ -75,21 +79,27 @@ def pick_num_attention_partitions(prompt_len: int, ntok: int, num_kv_heads: int,
     ``"reference"`` (mkm/scheduler.py:24-32): chunks of at least 256
     positions, at most ``min(W, 160) // kv_heads`` partitions.
 
-    ``"mi355x"``: chunks of at least 64 positions and at most ``min(W //
-    kv_heads, 25)`` partitions, trimmed so that none is empty.  The kernel's
-    partial attention is bound by its VALU work per workgroup (positions x
-    query heads per KV head), not by bandwidth, so on 256 compute units it
-    pays to spread the cache over more of them; 25 is what one terminal
-    reduction instruction can list.
+    ``"mi355x"``: chunks of at least 112 positions and at most ``min(W //
+    kv_heads, 25)`` partitions, trimmed so that none is empty.  A
+    workgroup's partial attention is bound by how fast it pulls its K/V rows
+    (and, for short partitions, by its fixed merge-and-store cost), not by
+    the HBM bandwidth of the whole chip, so on 256 compute units it pays to
+    spread the cache over more of them; 25 is what one terminal reduction
+    instruction can list.  ``"mi355x:N"`` caps the count at N instead.
     """
     seq = prompt_len + ntok
     if policy == "reference":
         chunks = math.ceil(seq / 256)
         cap = min(sm_count, ATTN_PARTITION_CAP) // num_kv_heads
         return max(1, min(chunks, cap))
-    if policy != "mi355x":
+    cap = MAX_REDUCTION_LIST
+    if policy.startswith("mi355x:"):
+        cap = int(policy.split(":", 1)[1])
+        if not 1 <= cap <= MAX_REDUCTION_LIST:
+            raise ValueError(f"partition cap must be in 1..{MAX_REDUCTION_LIST}, got {cap}")
+    elif policy != "mi355x":
         raise ValueError(f"unknown partition policy {policy!r}")
-    n = max(1, min(math.ceil(seq / 64), sm_count // num_kv_heads, MAX_REDUCTION_LIST))
+    n = max(1, min(math.ceil(seq / MIN_PARTITION_POSITIONS), sm_count // num_kv_heads, cap))
     total = math.ceil(seq / kv_block_size)
     return max(1, math.ceil(total / math.ceil(total / n)))
 

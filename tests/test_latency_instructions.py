@@ -100,7 +100,7 @@ def test_make_globals_buffers():
     assert g.skip_attn_reduction  # 21 positions: one partition
 
 
-@pytest.mark.parametrize("policy,parts", [("reference", 2), ("mi355x", 4)])
+@pytest.mark.parametrize("policy,parts", [("reference", 2), ("mi355x", 3)])
 def test_dag_structure(policy, parts):
     model = make_synthetic_llama(LLAMA_SMALL, "cpu", 0, kv_positions=400, prefill=300)
     g = make_globals(model, seq_len=300, sm_count=16, attention_partitions=policy)
@@ -122,9 +122,9 @@ def test_dag_structure(policy, parts):
 @pytest.mark.parametrize("seq,kv,W", [(1, 8, 256), (64, 8, 256), (65, 8, 256), (2049, 8, 256), (4097, 8, 256),
                                       (16385, 8, 256), (301, 4, 16), (1000, 2, 7)])
 def test_mi355x_partition_policy(seq, kv, W):
-    """At most min(W / kv, 25) partitions, none empty, more than 32
-    positions each on average (n = ceil(seq / 64) before the cap); the
-    reference policy is unchanged."""
+    """At most min(W / kv, 25) partitions, none empty, more than 56
+    positions each on average (n = ceil(seq / 112) before the cap); the
+    reference policy is unchanged; "mi355x:N" caps the count at N."""
     from megakernels_amd.mixtral.scheduler import pick_num_attention_partitions
     from oracle.python_vm import partial_token_range
 
@@ -134,6 +134,10 @@ def test_mi355x_partition_policy(seq, kv, W):
     assert all(b > a for a, b in ranges)
     assert [t for a, b in ranges for t in range(a, b)] == list(range(seq))
     if n < min(W // kv, 25):
-        assert n == 1 or seq / n > 32
+        assert n == 1 or seq / n > 56
+    for cap in (1, 8, 25):
+        assert pick_num_attention_partitions(seq, 0, kv, W, f"mi355x:{cap}") <= cap
+    with pytest.raises(ValueError):
+        pick_num_attention_partitions(seq, 0, kv, W, "mi355x:26")
     ref = pick_num_attention_partitions(seq, 0, kv, W)
     assert ref == max(1, min(math.ceil(seq / 256), min(W, 160) // kv))
