@@ -284,6 +284,9 @@ def decode_bench(args):
     gkw = {"attention_partitions": args.partitions}
     if args.qkv_block:
         gkw["qkv_block_size"] = args.qkv_block
+    for kv in args.block_size:
+        k, v = kv.split("=", 1)
+        gkw[k] = int(v)
     gen = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                              dag_kwargs=None if llama else {"predict": not args.no_predict},
                              device_argmax=not args.host_argmax)
@@ -337,6 +340,8 @@ def decode_bench(args):
             "predictor": None if llama else not args.no_predict,
             "assignment": args.assign,
             "qkv_block_size": g.qkv_block_size,
+            "block_sizes": {k: getattr(g, k) for k in ("up_gate_proj_block_size", "down_proj_block_size",
+                                                       "matvec_reduction_size") if hasattr(g, k)},
             "partition_policy": args.partitions,
             "argmax": "torch, between launches" if args.host_argmax else "in-kernel, with the next embedding",
         },
@@ -430,6 +435,9 @@ def main():
     ap.add_argument("--partitions", default="mi355x",
                     help="c3/c4/c5: split-KV partition policy: mi355x, mi355x:N (at most N partitions per KV head) "
                          "or reference")
+    ap.add_argument("--block-size", action="append", default=[], metavar="NAME=N",
+                    help="c3: override a dense-VM block size (up_gate_proj_block_size, down_proj_block_size, "
+                         "o_proj_block_size, lm_head_block_size, matvec_reduction_size)")
     ap.add_argument("--no-predict", action="store_true",
                     help="c4/c5: leave opcode 8 (expert prediction) and the early expert loads that use it out")
     ap.add_argument("--predict-sigma", type=float, default=None,

@@ -4,18 +4,19 @@ Counterpart of ``megakernels/demos/latency/scheduler.py:1-440``:
 
 * ``make_globals`` allocates the reference's buffers with the same shapes and
   dtypes (``:39-147``): barriers ``[L, 10, Hq + 2*Hkv]`` int32, ``silu_out
-  [F]``, attention intermediates sized by the worker count, block sizes 16
-  and ``matvec_reduction_size = gcd(F, H)``.
+  [F]``, attention intermediates sized by the worker count, block sizes 16;
+  ``matvec_reduction_size`` is F / 4 where the kernel takes that width
+  (``default_reduction_size``; the reference's gcd(F, H) otherwise).
 * the partitioners follow ``:150-264``: QKV and LM-head blocks in contiguous
   banker's-rounded spans, up/gate blocks strided by the worker count, and
   down-projection (column chunk, row block) jobs split over workers so that
   each instruction stays within one column chunk.
 * ``make_dag`` builds the per-layer DAG of ``:267-428``.
-* ``qkv_block_size`` is picked for the worker count among 16 and 8 rows
-  (``pick_block_size``: at 3B and 256 workers, 8-row blocks give every
-  worker at most 24 QKV rows where the reference's 16-row blocks leave 32 on
-  some and 16 on others; 4-row blocks measured slower), and the
-  split-KV partition count follows the MI355X policy of the Mixtral
+* ``qkv_block_size`` is 16 rows, as in the reference: the kernel stages a
+  QKV block's rows on chip before its wait, and 16-row blocks measured
+  faster than the 8-row ones that balance the row count (at 3B and 256
+  workers: 24 rows on every worker instead of 32 on some and 16 on others).
+  The split-KV partition count follows the MI355X policy of the Mixtral
   scheduler; ``attention_partitions="reference"`` restores the reference's.
 
 The reference asserts more than one block per worker in every partitioner
@@ -33,7 +34,7 @@ import torch
 from ..instructions import NoOp
 from ..scheduler import DAG_Node, ScheduleBuilder
 from ..utils import assert_div, get_sm_count
-from ..mixtral.scheduler import pick_block_size, pick_num_attention_partitions
+from ..mixtral.scheduler import pick_num_attention_partitions
 from .instructions import (
     AttentionReduction,
     DownProjResidual,
@@ -49,15 +50,37 @@ from .instructions import (
 BARRIER_OPS = 10
 
 
+def default_reduction_size(intermediate: int, hidden: int) -> int:
+    """Column chunk of the dense down-projection (``matvec_reduction_size``):
+    a quarter of the FFN width when that is 512, 1024, 2048 or 4096 columns,
+    else gcd(F, H) as before.  Four chunks per row measured best at the 3B
+    shape (F = 8192: 2048 -> 547.3 tokens/s, 1024 -> 528.2, 4096 -> 540.5,
+    512 -> 489.8): each chunk of a row is a separate job whose partial is
+    added into the residual with a packed bf16 atomic, so fewer chunks mean
+    fewer jobs and atomics, and more mean more parallelism."""
+    r = intermediate // 4
+    if intermediate % 4 == 0 and r in (512, 1024, 2048, 4096):
+        return r
+    return math.gcd(intermediate, hidden)
+
+
 def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 0,
                  sm_count: int | None = None, attention_partitions: str = "mi355x",
-                 qkv_block_size: int | None = None) -> Globals:
+                 qkv_block_size: int | None = None, **block_sizes) -> Globals:
     """Activation buffers plus ``model``'s stacked weights (duck-typed like
     the reference's ``LlamaForCausalLM``); ``sm_count`` overrides the device
     query (needed when the globals live on the CPU); ``attention_partitions``
     is the split-KV partition policy (the Mixtral scheduler's
     ``pick_num_attention_partitions``; ``"reference"`` reproduces the
-    reference's instruction list)."""
+    reference's instruction list).  ``block_sizes`` override the defaults of
+    ``up_gate_proj_block_size``, ``down_proj_block_size``,
+    ``o_proj_block_size``, ``lm_head_block_size`` and
+    ``matvec_reduction_size``."""
+    allowed = {"up_gate_proj_block_size", "down_proj_block_size", "o_proj_block_size", "lm_head_block_size",
+               "matvec_reduction_size"}
+    unknown = set(block_sizes) - allowed
+    if unknown:
+        raise TypeError(f"unknown block sizes {sorted(unknown)}")
     cfg = model.config
     device = torch.device(model.device)
     dtype = model.dtype
@@ -105,13 +128,16 @@ def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 
         silu_out=buf(cfg.intermediate_size),
         logits=buf(cfg.vocab_size),
         skip_attn_reduction=skip_attn_reduction,
-        up_gate_proj_block_size=16,
-        down_proj_block_size=16,
-        o_proj_block_size=16,
-        lm_head_block_size=16,
-        matvec_reduction_size=math.gcd(cfg.intermediate_size, cfg.hidden_size),
-        qkv_block_size=qkv_block_size or pick_block_size((Hq + 2 * Hkv) * D, workers,
-                                                         tuple(b for b in (16, 8) if D % b == 0)),
+        up_gate_proj_block_size=block_sizes.get("up_gate_proj_block_size", 16),
+        down_proj_block_size=block_sizes.get("down_proj_block_size", 16),
+        o_proj_block_size=block_sizes.get("o_proj_block_size", 16),
+        lm_head_block_size=block_sizes.get("lm_head_block_size", 16),
+        matvec_reduction_size=block_sizes.get("matvec_reduction_size",
+                                              default_reduction_size(cfg.intermediate_size, cfg.hidden_size)),
+        # 16-row QKV blocks: the kernel stages a block's rows on chip before
+        # its wait, so fewer, larger blocks pay (config 3: 547.3 -> 550.4
+        # tokens/s against 8-row blocks)
+        qkv_block_size=qkv_block_size or (16 if D % 16 == 0 else 8),
         attn_kv_block_size=16,
         attn_reduction_size=Hq // Hkv,
     )
