@@ -289,7 +289,7 @@ def decode_bench(args):
         gkw[k] = int(v)
     gen = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                              dag_kwargs=None if llama else {"predict": not args.no_predict},
-                             device_argmax=not args.host_argmax)
+                             device_argmax=not args.host_argmax, reset_next=not args.no_reset)
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
@@ -344,6 +344,7 @@ def decode_bench(args):
                                                        "matvec_reduction_size") if hasattr(g, k)},
             "partition_policy": args.partitions,
             "argmax": "torch, between launches" if args.host_argmax else "in-kernel, with the next embedding",
+            "fills_between_launches": args.host_argmax or args.no_reset,
         },
         "roofline": {
             "bound": "hbm",
@@ -445,6 +446,9 @@ def main():
     ap.add_argument("--host-argmax", action="store_true",
                     help="c3/c4/c5: torch.argmax and the embedding lookup between launches, as the reference's "
                          "generator (default: inside the launch)")
+    ap.add_argument("--no-reset", action="store_true",
+                    help="c3/c4/c5: fill the barriers and logits before every launch instead of having each "
+                         "launch zero them for the next")
     ap.add_argument("--no-skewed", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))

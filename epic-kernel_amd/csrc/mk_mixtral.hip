@@ -164,6 +164,9 @@ struct KParams {
     // the embedding table into hidden (the next step's input)
     int64_t *argmax_out;
     const uint16_t *next_embed;
+    // with argmax_out: the last workgroup also zeroes the barrier tensor (1)
+    // and the logits (2) for the next launch
+    int32_t reset_next;
     // dense VM: opcode-5 items (gate and up rows) that opcode 4 stages in LDS
     // while it waits, and where (u32x4 index into the dynamic LDS); 0: off
     int32_t stage_items;
@@ -2340,6 +2343,17 @@ __device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
     }
 }
 
+// Zero n 32-bit words at p (4-byte aligned) with the workgroup: 16-byte
+// stores from the first 16-byte boundary on.
+__device__ __forceinline__ void zero_words(uint32_t *p, size_t n) {
+    const size_t head = min(n, (size_t)((16u - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / 4);
+    if (threadIdx.x < head) p[threadIdx.x] = 0u;
+    u32x4 *v = reinterpret_cast<u32x4 *>(p + head);
+    const size_t nv = (n - head) / 4;
+    for (size_t i = threadIdx.x; i < nv; i += kThreads) v[i] = u32x4{0u, 0u, 0u, 0u};
+    for (size_t i = head + nv * 4 + threadIdx.x; i < n; i += kThreads) p[i] = 0u;
+}
+
 // Exit protocol: the last workgroup out (failed or not) zeroes the
 // work-sharing counters for the next launch, after the decode-driver tail
 // when one was asked for.  Every other workgroup has finished all of its
@@ -2353,6 +2367,16 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
     __syncthreads();
     if (sh.flag) {
         if (p.argmax_out != nullptr && p.ap != nullptr && !aborted(p)) exit_argmax(p, sh);
+        if (p.reset_next > 0) {
+            // every other workgroup is done with the barriers, and the
+            // argmax above has read the logits
+            zero_words(reinterpret_cast<uint32_t *>(p.bar), (size_t)p.num_layers * p.bar_ops * p.bar_width);
+            if (p.reset_next > 1 && p.ap != nullptr) {
+                attn_c &a = attn_of(p);
+                zero_words(reinterpret_cast<uint32_t *>(a.logits), (size_t)(a.V >> 1));
+                if ((a.V & 1) && threadIdx.x == 0) a.logits[a.V - 1] = 0;
+            }
+        }
         const int n = 2 * (int)gridDim.x * p.queue_len;
         for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
         drain_and_sync();
@@ -2810,6 +2834,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.down_arrivals = (g->intermediate_size / g->matvec_reduction_size) * (g->hidden_size / g->down_proj_block_size);
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
+    kp.reset_next = g->reset_for_next_launch ? 1 : 0;
     kp.attn = 1;
     AttnParams a{};
     a.qkv = g->qkv_weights;
@@ -2944,6 +2969,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.lds_bytes = (int32_t)lds;
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
+    kp.reset_next = g->reset_for_next_launch ? (g->qkv_weights != nullptr ? 2 : 1) : 0;
     kp.attn = g->qkv_weights != nullptr;
     kp.ap = nullptr;
     if (kp.attn) {

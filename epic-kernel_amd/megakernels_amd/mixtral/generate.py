@@ -13,8 +13,10 @@ The argmax and the next step's embedding run inside the launch
 workgroup writes the token straight into ``output_tokens`` and copies its
 embedding row into ``hidden_states``, where the reference runs
 ``torch.argmax`` and the embedding lookup between launches
-(``megakernels/generators.py:121-145``).  ``device_argmax=False`` restores
-the torch calls.
+(``megakernels/generators.py:121-145``).  It also zeroes the barriers and
+the logits for the next launch (``reset_for_next_launch``), so a step after
+the first enqueues the launch alone (``reset_next=False`` keeps the fills).
+``device_argmax=False`` restores the torch calls and the fills.
 
 The schedule is built once (``make_dag`` over all layers plus the LM head)
 and reused for every position; partial-attention instructions cover the
@@ -34,14 +36,17 @@ from .scheduler import make_dag, make_globals
 
 class MK_Generator:
     def __init__(self, model, interpreter: MixtralMK_Interpreter, schedule: Schedule, barrier_fill_val: int = 0,
-                 device_argmax: bool = True, **launch_kwargs):
+                 device_argmax: bool = True, reset_next: bool = True, **launch_kwargs):
         self.model = model
         self.interpreter = interpreter
         self.schedule = schedule
         self.barrier_fill_val = barrier_fill_val
         self.device_argmax = device_argmax
+        self.reset_next = reset_next and barrier_fill_val == 0
         self.launch_kwargs = launch_kwargs
         self.fill()
+        # the barriers and logits are zero (the last launch reset them)
+        self._clean = False
 
     @classmethod
     def build(cls, model, prompt_len: int, mode: str = "rr", sm_count: int | None = None, dag_kwargs=None,
@@ -86,17 +91,21 @@ class MK_Generator:
         globs = self.schedule.globs
         if not embedded:
             globs.hidden_states.copy_(self.model.embed_tokens[input_ids.reshape(-1)[0]])
-        self.fill()
+        if not self._clean:
+            self.fill()
+            globs.logits.zero_()
         globs.pos_id = pos_id
-        globs.logits.zero_()
         if not self.device_argmax:
+            self._clean = False
             self.interpreter.interpret(globs, **self.launch_kwargs)
             return torch.argmax(globs.logits, dim=-1)
         if out is None:
             out = torch.empty((), dtype=torch.long, device=globs.logits.device)
+        self._clean = False
         self.interpreter.interpret(globs, argmax_out=out,
                                    next_embed_weights=self.model.embed_tokens if embed_next else None,
-                                   **self.launch_kwargs)
+                                   reset_for_next_launch=self.reset_next, **self.launch_kwargs)
+        self._clean = self.reset_next
         return out
 
     def generate(self, output_tokens: torch.Tensor, prompt_len: int, ntok: int, ntok_already_generated: int = 1):

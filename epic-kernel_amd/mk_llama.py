@@ -13,8 +13,8 @@ under the reference's 3B module name.
 Keyword-only additions (defaults are the reference's compiled-in values):
 the block sizes and ``matvec_reduction_size`` the instructions were built
 with, ``spin_timeout_us``, ``record_timings``, ``argmax_out`` /
-``next_embed_weights`` and ``debug_sync`` (as in ``mk_mixtral``).  There is
-no fallback.
+``next_embed_weights``, ``reset_for_next_launch`` and ``debug_sync`` (as in
+``mk_mixtral``).  There is no fallback.
 """
 
 from __future__ import annotations
@@ -91,6 +91,7 @@ class MkLlamaGlobals(ctypes.Structure):
         ("record_timings", ctypes.c_int32),
         ("argmax_out", ctypes.c_void_p),
         ("next_embed_weights", ctypes.c_void_p),
+        ("reset_for_next_launch", ctypes.c_int32),
     ]
 
 
@@ -134,6 +135,7 @@ def build_llama_struct(
     record_timings: bool = False,
     argmax_out=None,
     next_embed_weights=None,
+    reset_for_next_launch: bool = False,
 ) -> MkLlamaGlobals:
     """Validate the reference-ordered arguments and fill the C struct;
     ``TypeError``/``ValueError`` before anything reaches the GPU."""
@@ -239,6 +241,7 @@ def build_llama_struct(
     g.spin_timeout_us = int(spin_timeout_us)
     g.record_timings = int(bool(record_timings))
     g.argmax_out, g.next_embed_weights = mk_mixtral._decode_tail(argmax_out, next_embed_weights, True, dev, H)
+    g.reset_for_next_launch = int(bool(reset_for_next_launch))
     return g
 
 

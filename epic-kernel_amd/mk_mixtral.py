@@ -31,6 +31,9 @@ sizes are the compile-time 16):
     order) into the int64 ``argmax_out``, and with the ``[V, H]`` embedding
     table sets ``hidden_states`` to that token's row, the next step's input
     -- what the reference's generator does with torch between launches;
+``reset_for_next_launch``
+    the launch ends by zeroing the barrier tensor and the logits, so that
+    the next launch needs no fill (neither can be read afterwards);
 ``debug_sync``
     synchronise after the launch and raise :class:`MKDeviceError` if the
     kernel recorded a failure.
@@ -166,6 +169,7 @@ class MkMixtralGlobals(ctypes.Structure):
         ("work_sharing", ctypes.c_int32),
         ("argmax_out", _P),
         ("next_embed_weights", _P),
+        ("reset_for_next_launch", ctypes.c_int32),
     ]
 
 
@@ -318,6 +322,7 @@ def build_globals_struct(
     work_sharing: bool = False,
     argmax_out=None,
     next_embed_weights=None,
+    reset_for_next_launch: bool = False,
 ) -> MkMixtralGlobals:
     """Validate the reference-ordered arguments and fill the C struct.
 
@@ -430,6 +435,7 @@ def build_globals_struct(
     g.record_timings = int(bool(record_timings))
     g.work_sharing = int(bool(work_sharing))
     g.argmax_out, g.next_embed_weights = _decode_tail(argmax_out, next_embed_weights, attn is not None, dev, H)
+    g.reset_for_next_launch = int(bool(reset_for_next_launch))
     return g
 
 

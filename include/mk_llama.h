@@ -123,6 +123,8 @@ typedef struct mk_llama_globals {
      * megakernels/generators.py:121-145), as in mk_mixtral_globals */
     int64_t *argmax_out;                /* argmax of logits when the launch ends, or NULL */
     const uint16_t *next_embed_weights; /* [V, H] bf16 or NULL: hidden_states := row *argmax_out */
+    int32_t reset_for_next_launch;      /* nonzero: the barrier tensor is zeroed when the launch ends
+                                           (the logits are stored, not accumulated, and need none) */
 } mk_llama_globals;
 
 /* Launch one decode step of the dense VM.  Returns MK_OK or an

@@ -212,6 +212,11 @@ typedef struct mk_mixtral_globals {
     const uint16_t *next_embed_weights; /* [V, H] bf16, needs argmax_out: when
                                       the launch ends, hidden_states := row
                                       *argmax_out (the next step's input) */
+    int32_t reset_for_next_launch; /* nonzero: when the launch ends, the
+                                      barrier tensor (its num_layers layers)
+                                      and the logits are zeroed, so the next
+                                      launch needs no fill; the caller then
+                                      cannot read either */
 } mk_mixtral_globals;
 
 /* Launch one persistent-kernel pass over the instruction queues.

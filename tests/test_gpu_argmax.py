@@ -97,3 +97,39 @@ def test_argmax_alone_leaves_hidden(dense):
         assert int(out[0]) == ref_token
         assert torch.equal(hidden, ref_hidden)
     assert not torch.equal(hidden, case.gpu_model.embed_tokens[int(out[0])])
+
+
+@pytest.mark.parametrize("dense", [False, True], ids=["mixtral", "llama"])
+def test_reset_for_next_launch(dense):
+    """reset_for_next_launch: the launch ends with the barrier tensor zeroed
+    (and the Mixtral logits, which the LM head accumulates); the token is
+    the argmax of the logits before the reset, and the next launch, started
+    without any fill, gives the same results as one after a fill."""
+    case = (LlamaCase(LLAMA_TINY, seed=33, prefill=40, steps=2) if dense
+            else FullCase(TINY, seed=33, prefill=40, steps=2))
+    g = case.g_gpu
+    _launch(case, dense, 11)
+    ref_token = int(torch.argmax(g.logits.cpu()))
+    ref_hidden = g.hidden_states.clone()
+    out = torch.full((), -1, dtype=torch.long, device="cuda")
+    _launch(case, dense, 11, argmax_out=out, reset_for_next_launch=True)
+    assert int(out) == ref_token
+    assert int(g.barriers.abs().sum()) == 0
+    if not dense:
+        assert not g.logits.any()
+    # next launch straight away, no fill: same hidden state as a filled one
+    g.hidden_states.copy_(case.gpu_model.embed_tokens[11])
+    from megakernels_amd.latency.mk import interpret_with_mk as run_dense
+    from megakernels_amd.mixtral.mk import interpret_with_mk as run_moe
+    import mk_llama
+    import mk_mixtral
+
+    if dense:
+        run_dense(g, mk_llama.mk_llama, debug_sync=True)
+    else:
+        run_moe(g, mk_mixtral.mk_mixtral, debug_sync=True)
+    torch.cuda.synchronize()
+    if dense:
+        assert max_abs_rel(g.hidden_states, ref_hidden) <= 2e-2
+    else:
+        assert torch.equal(g.hidden_states, ref_hidden)
