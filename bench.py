@@ -64,7 +64,7 @@ class MoEBench:
     """Per-token launches of the MoE-only schedule over resident inputs."""
 
     def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, work_sharing: bool = False,
-                 balance: bool = False, calib_tokens: int = 16):
+                 balance: bool = False, calib_tokens: int = 16, moe_overlap: str = "off", upgate_rounds: int = 3):
         import torch
 
         import mk_mixtral
@@ -80,7 +80,8 @@ class MoEBench:
         self.residuals = make_residuals(tokens, cfg.hidden_size, generator=self.model.generator)
         # speed-balanced partitions need row-granular blocks
         bs = dict(expert_proj_block_size=1, down_proj_block_size=1) if balance else {}
-        self.globs = g = make_globals(self.model, **bs)
+        self.globs = g = make_globals(self.model, moe_overlap=moe_overlap in ("on", "op5"),
+                                      upgate_rounds=upgate_rounds, **bs)
         nodes, end = make_moe_dag(g)
         self.schedule = Schedule(g, nodes, end)
         self.queues = assign_to_sms("rr", schedule=self.schedule)
@@ -101,7 +102,7 @@ class MoEBench:
             kw.pop("stream", None)
             captured["g"] = mk_mixtral.build_globals_struct(*args, **kw)
 
-        interpret_with_mk(g, capture, work_sharing=work_sharing)
+        interpret_with_mk(g, capture, work_sharing=work_sharing, downproj_overlap=moe_overlap in ("on", "op6"))
         self.struct = captured["g"]
         self.lib = mk_mixtral.load_library()
         self.mk = mk_mixtral
@@ -453,6 +454,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--moe-overlap", choices=["on", "off", "op5", "op6"], default="off",
+                    help="c1/c2: interleaved opcode-5 partition with opcode 6 starting on finished SiLU "
+                         "column groups (on), the reference's contiguous partition and full barrier (off), "
+                         "or one half alone: the interleaved partition with the full barrier (op5), the "
+                         "grouped opcode 6 on the contiguous partition (op6)")
+    ap.add_argument("--upgate-rounds", type=int, default=3,
+                    help="c1/c2 with --moe-overlap on/op5: contiguous opcode-5 block runs per worker")
     ap.add_argument("--balance", action="store_true",
                     help="re-split rows by per-worker speed measured on a few launches (block size 1)")
     ap.add_argument("--work-sharing", action="store_true",
@@ -490,7 +498,9 @@ def main():
 
     cfg = C2 if args.config == "c2" else C1
     print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
-    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance)
+    overlap = args.moe_overlap
+    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
+                     moe_overlap=overlap, upgate_rounds=args.upgate_rounds)
     timed = run_timed(bench, args.steps, args.warmup)
     dist = bench.per_launch_us(256)
     if args.trace:
@@ -503,7 +513,7 @@ def main():
     skewed = None
     if not args.no_skewed:
         sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
-                      router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
+                      moe_overlap=overlap, upgate_rounds=args.upgate_rounds, router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
         sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
         sk_us = sk_timed["us_per_launch_events"]
         skewed = {"moe_layer_us": sk_us, "hbm_frac": nbytes / (sk_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
@@ -543,6 +553,7 @@ def main():
             "down_proj_block_size": g.down_proj_block_size,
             "work_sharing": args.work_sharing,
             "speed_balanced_partition": args.balance,
+            "moe_overlap": overlap,
         },
         "moe_layer_us": us,
         "moe_layer_us_per_launch": dist,

@@ -110,6 +110,17 @@ constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) tha
 static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
 constexpr int kRowBatchLds = 64;  // rows per opcode-6 batch (partial sums in LDS)
 constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 16 * 512)
+constexpr int kMaxMerge = 8;      // consecutive opcode-5 instructions of a layer run as one item pool
+#ifndef MK_GROUP_CHUNKS
+#define MK_GROUP_CHUNKS 7
+#endif
+#ifndef MK_ITEM_ROWS
+#define MK_ITEM_ROWS 1
+#endif
+constexpr int kGroupChunks = MK_GROUP_CHUNKS;  // overlapped opcode 6: 512-column chunks per column group
+constexpr int kItemRows = MK_ITEM_ROWS;        // overlapped opcode 6: rows per item (both experts)
+constexpr int kMaxGroups = 8;     // overlapped opcode 6: column groups per row (F <= 8 * 4 * 512)
+static_assert(kRowBatchLds * 2 * kMaxSegments >= 32 * 2 * kMaxGroups, "overlapped opcode-6 partials fit in sh.part");
 
 static_assert(kThreads % 64 == 0 && kThreads <= 1024, "wave64 workgroup");
 
@@ -172,6 +183,12 @@ struct KParams {
     int32_t stage_items;
     int32_t stage_off16;
     int32_t lds_bytes;  // dynamic LDS of the launch
+    // opcode-5/6 overlap (NULL: off): finished SiLU rows of both selected
+    // experts per (layer, 512-row column chunk of F), counted by opcode 5 as
+    // its instructions complete; opcode 6 then starts on the column groups
+    // that are complete instead of waiting for the whole layer
+    int32_t *chunk_ctr;
+    int32_t scratch_clear;  // scratch ints from kScratchSlotBase the last workgroup zeroes
 };
 
 struct AttnParams {
@@ -213,6 +230,10 @@ struct SharedState {
     // dense VM: queue slot whose first stage_n opcode-5 items opcode 4 staged
     // in LDS (-1: none)
     int stage_slot, stage_n;
+    // opcode 5 over consecutive instructions of one layer (kMaxMerge at
+    // most): first FFN row, rows, first pooled item, finished items
+    int grp_row0[kMaxMerge], grp_nrows[kMaxMerge], grp_first[kMaxMerge + 1], grp_done[kMaxMerge];
+    int ready_mask;  // opcode 6: column groups whose SiLU rows are complete
 };
 
 struct Ctx {
@@ -811,12 +832,36 @@ __device__ __forceinline__ void steal_upgate(const KParams &p, const SharedState
     }
 }
 
+// Count a finished item of pooled instruction k (lane 0; the wave's SiLU
+// stores of it have completed).  The item that completes the instruction
+// arrives for its blocks on the layer counter and, with the overlap on, adds
+// its rows to the column-chunk counters.
+__device__ __forceinline__ void upgate_item_done(const KParams &p, SharedState &sh, int layer, int k, int lane) {
+    if (lane != 0 || k < 0) return;
+    const int r0 = sh.grp_row0[k], n = sh.grp_nrows[k];
+    if (atomicAdd(&sh.grp_done[k], 1) + 1 != 2 * n) return;
+    __hip_atomic_fetch_add(bar_at(p, layer, 5), n / p.expert_bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (p.chunk_ctr != nullptr) {
+        int32_t *cc = p.chunk_ctr + (size_t)layer * (p.F / kChunkElems);
+        for (int r = r0; r < r0 + n;) {
+            const int ch = r / kChunkElems, e = min(r0 + n, (ch + 1) * kChunkElems);
+            __hip_atomic_fetch_add(cc + ch, e - r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            r = e;
+        }
+    }
+}
+
+// `consumed` returns the queue slots handled: without work sharing, the
+// instructions of the same layer that follow this one in the worker's queue
+// (kMaxMerge at most) run as one pool of items, so the routing is computed
+// once and no wave waits for another between them.
 template <int kE, bool kSpec>
 __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
-                                                     const Ctx &c, int32_t *tim) {
+                                                     const Ctx &c, int32_t *tim, int &consumed) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
     const int nb = __builtin_amdgcn_readfirstlane(ins[3]);
+    consumed = 1;
     if (layer < 0 || layer >= p.num_layers || start < 0 || nb < 0 ||
         (int64_t)(start + nb) * p.expert_bs > (int64_t)p.F) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 5, layer, start, nb);
@@ -824,6 +869,49 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     }
     // an empty instruction owns no rows (another one starts at block 0)
     if (nb == 0) return true;
+    int K = 1;
+    bool pub = start == 0;  // the pool holds the instruction that starts at block 0
+    if (!p.work_sharing) {
+        // the next kMaxMerge - 1 slots' words, read without a dependency
+        // between them (slot indices clamped to the queue: one round trip);
+        // whole-model kernels (kSpec) run one instruction at a time, which
+        // keeps their registers within the budget
+        constexpr int kPool = kSpec ? 1 : kMaxMerge;
+        int st_k[kPool], nb_k[kPool];
+        bool more = true;
+        st_k[0] = start;
+        nb_k[0] = nb;
+#pragma unroll
+        for (int k = 1; k < kPool; ++k) {
+            ins_t *n = ins + (min(c.slot + k, p.queue_len - 1) - c.slot) * MK_INTS_PER_INSTRUCTION;
+            const int op_n = __builtin_amdgcn_readfirstlane(n[0]);
+            const int layer_n = __builtin_amdgcn_readfirstlane(n[1]);
+            st_k[k] = __builtin_amdgcn_readfirstlane(n[2]);
+            nb_k[k] = __builtin_amdgcn_readfirstlane(n[3]);
+            // an out-of-range instruction ends the pool and reports itself
+            more = more && c.slot + k < p.queue_len && op_n == 5 && layer_n == layer && st_k[k] >= 0 &&
+                   nb_k[k] > 0 && (int64_t)(st_k[k] + nb_k[k]) * p.expert_bs <= (int64_t)p.F;
+            if (more) {
+                pub = pub || st_k[k] == 0;
+                ++K;
+            }
+        }
+        if (threadIdx.x == 0) {
+            int first = 0;
+#pragma unroll
+            for (int k = 0; k < kPool; ++k) {
+                if (k < K) {
+                    sh.grp_row0[k] = st_k[k] * p.expert_bs;
+                    sh.grp_nrows[k] = nb_k[k] * p.expert_bs;
+                    sh.grp_first[k] = first;
+                    sh.grp_done[k] = 0;
+                    first += 2 * nb_k[k] * p.expert_bs;
+                }
+            }
+            sh.grp_first[K] = first;
+        }
+    }
+    consumed = K;
     RouterRegs<kE> rr;
     router_prefetch<kE>(p, sh, layer, p.router, rr);
     // items 0 .. kWaves-1 go to waves 0 .. kWaves-1, the rest through the
@@ -894,7 +982,7 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     }
     // Exactly one instruction per layer starts at block 0: it publishes the
     // normed hidden state and the routing decision.
-    if (start == 0) {
+    if (pub) {
         u32x4 *out = reinterpret_cast<u32x4 *>(p.normed_out);
         for (int v = tid; v < (p.H >> 3); v += kThreads) st_dev128(out + v, act[v]);
         if (tid == 0) {
@@ -903,6 +991,8 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
             st_dev16(p.sel_score, sc0);
             st_dev16(p.sel_score + 1, sc1);
         }
+        // pooled instructions arrive one by one: publish before any of them
+        if (!p.work_sharing) drain_and_sync();
     }
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
@@ -933,18 +1023,44 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
         // Waves take items from a workgroup counter in LDS rather than a
         // fixed stride: the memory pipeline favours older waves, so with a
         // fixed split the youngest wave ends up finishing its last items
-        // alone.
-        int k = 0;
-        for (int it = wave; it < 2 * nrows; ++k) {
-            upgate_item(p, act, layer, row0, nrows, t.i0, t.i1, it, lane);
+        // alone.  An item is counted once the next one's weights have been
+        // used: its SiLU store has then completed (a wait for it costs
+        // nothing there), so no wave stops streaming to publish rows.
+        const int total = __builtin_amdgcn_readfirstlane(sh.grp_first[K]);
+        int k = 0, pending = -1;
+        for (int it = wave; it < total; ++k) {
+            int q = 0;
+            while (q + 1 < K && it >= __builtin_amdgcn_readfirstlane(sh.grp_first[q + 1])) ++q;
+            const int local = it - __builtin_amdgcn_readfirstlane(sh.grp_first[q]);
+            const int r0 = __builtin_amdgcn_readfirstlane(sh.grp_row0[q]);
+            const int nr = __builtin_amdgcn_readfirstlane(sh.grp_nrows[q]);
+            const int j = local >= nr;
+            const int r = r0 + (j ? local - nr : local);
+            const int e = j ? t.i1 : t.i0;
+            const size_t off = ((size_t)(layer * p.E + e) * p.F + r) * (size_t)p.H;
+            float ag = 0.f, au = 0.f;
+            dot_pair(p.gate + off, p.up + off, act, act, p.H / kChunkElems, lane, ag, au);
+            ag = wave_sum(ag);
+            au = wave_sum(au);
+            __builtin_amdgcn_s_waitcnt(0);
+            upgate_item_done(p, sh, layer, pending, lane);
+            silu_store(p, e, r, ag, au, lane);
+            pending = q;
             // per-item completion times of waves 0 and 7 (timing record only)
             if (tim != nullptr && lane == 0 && (wave == 0 || wave == kWaves - 1) && k < 16)
                 tim[64 + (wave ? 16 : 0) + k] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
             it = next_local_item(sh, lane);
         }
+        __builtin_amdgcn_s_waitcnt(0);
+        upgate_item_done(p, sh, layer, pending, lane);
         drain_and_sync();
-        arrive(bar_at(p, layer, 5), nb);
         stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+        // the pooled slots share this one's times
+        if (tim != nullptr && threadIdx.x == 0)
+            for (int m = 1; m < K; ++m) {
+                tim[m * MK_TIMING_SLOTS + MK_TEVENT_START] = tim[MK_TEVENT_START];
+                tim[m * MK_TIMING_SLOTS + MK_TEVENT_END] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
+            }
     }
     return true;
 }
@@ -1012,6 +1128,150 @@ __device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 
     return acc;
 }
 
+// Opcode 6 overlapped with the end of opcode 5 (chunk counters on, and this
+// workgroup routed the layer itself, so the experts are known).  The SiLU
+// columns are taken in fixed groups of kGroupChunks 512-column chunks: as
+// soon as every row of a group is final (its chunk counters are full), the
+// group's SiLU values are staged in LDS and the instruction's rows are dotted
+// with them, a row pair and both experts per item (16 loads per lane in
+// flight).  The partial sum of each (row, expert, group) goes to LDS, and
+// the row's total is summed over the groups in a fixed order, so the result
+// does not depend on when a group became ready.
+__device__ __forceinline__ bool downproj_overlapped(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+                                                    int32_t *tim, int layer, int start, int end) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = start * p.down_bs, nrows = (end - start) * p.down_bs;
+    const int nc = p.F / kChunkElems;
+    const int ng = (nc + kGroupChunks - 1) / kGroupChunks;
+    const int nv = p.F >> 3;
+    const int npairs = nrows / kItemRows;
+    const int e0 = sh.route_idx[0], e1 = sh.route_idx[1];
+    const float s0 = sh.route_score[0], s1 = sh.route_score[1];
+    // opcode 5 ran here, after the O-projection barrier: the residual rows
+    // are final
+    uint32_t hpre = 0;
+    if (tid < nrows) hpre = ld_dev16(p.hidden + row0 + tid);
+    const int32_t *cc = p.chunk_ctr + (size_t)layer * nc;
+    const uint16_t *a0 = p.silu + (size_t)e0 * p.F;
+    const uint16_t *a1 = p.silu + (size_t)e1 * p.F;
+    const uint16_t *w0 = p.down + ((size_t)(layer * p.E + e0) * p.H + row0) * (size_t)p.F;
+    const uint16_t *w1 = p.down + ((size_t)(layer * p.E + e1) * p.H + row0) * (size_t)p.F;
+    const uint32_t all = (1u << ng) - 1u;
+    uint32_t done = 0;
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    while (done != all) {
+        // thread 0 polls until a group not yet done is complete
+        if (tid == 0) {
+            uint32_t ready = 0;
+            int ok = 1, nap = 1;
+            uint64_t t0 = 0;
+            for (;;) {
+                for (int g = 0; g < ng; ++g) {
+                    if ((done >> g) & 1u) continue;
+                    bool full = true;
+                    for (int k = 0; k < kGroupChunks; ++k) {
+                        const int ch = g * kGroupChunks + k;
+                        if (ch < nc && (int)ld_dev32(cc + ch) < kChunkElems) full = false;
+                    }
+                    if (full) ready |= 1u << g;
+                }
+                if (ready != 0) break;
+                if (aborted(p)) {
+                    ok = 0;
+                    break;
+                }
+                const uint64_t now = __builtin_amdgcn_s_memrealtime();
+                if (t0 == 0) {
+                    t0 = now;
+                } else if (now - t0 > (uint64_t)p.timeout_ticks) {
+                    report_error_lane(p, MK_ERR_TIMEOUT, c, 6, layer, (int)all, (int)done);
+                    ok = 0;
+                    break;
+                }
+                for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
+                if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
+            }
+            sh.ready_mask = ok ? (int)ready : -1;
+        }
+        __syncthreads();
+        const int rm = __builtin_amdgcn_readfirstlane(sh.ready_mask);
+        if (rm < 0) return false;
+        const uint32_t fresh = (uint32_t)rm;
+        // the fresh groups' SiLU values of both experts, at their offsets
+        for (int v = tid; v < nv; v += kThreads) {
+            if ((fresh >> ((v >> 6) / kGroupChunks)) & 1u) {
+                act[v] = ld_dev128(a0, (uint32_t)v * 16u);
+                act[nv + v] = ld_dev128(a1, (uint32_t)v * 16u);
+            }
+        }
+        if (tid == 0) sh.next_item = kWaves;
+        __syncthreads();
+        const int items = __popc(fresh) * npairs;
+        for (int it = wave; it < items; it = next_local_item(sh, lane)) {
+            uint32_t m = fresh;
+            for (int k = it / npairs; k > 0; --k) m &= m - 1u;
+            const int g = __builtin_ctz(m);
+            const int pr = it % npairs;
+            const int c0 = g * kGroupChunks, n = min(kGroupChunks, nc - c0);
+            // i = 0 .. 2 kItemRows - 1: row kItemRows pr + (i >> 1) of expert slot i & 1
+            const size_t roff = (size_t)(kItemRows * pr) * p.F + (size_t)(c0 * kChunkElems + lane * 8);
+            u32x4 w[2 * kItemRows][kGroupChunks];
+#pragma unroll
+            for (int i = 0; i < 2 * kItemRows; ++i) {
+                const u32x4 *rw = reinterpret_cast<const u32x4 *>(((i & 1) ? w1 : w0) + roff + (i >> 1) * (size_t)p.F);
+                // a short last group loads its last chunk again in place of the
+                // missing ones and drops them from the sums (selects, no
+                // branches: conditional loads here put the array in scratch)
+#pragma unroll
+                for (int k = 0; k < kGroupChunks; ++k) w[i][k] = load_stream(rw + min(k, n - 1) * 64);
+            }
+            float acc[2 * kItemRows];
+#pragma unroll
+            for (int i = 0; i < 2 * kItemRows; ++i) {
+                const u32x4 *x = act + ((i & 1) ? nv : 0) + c0 * 64 + lane;
+                acc[i] = 0.f;
+#pragma unroll
+                for (int k = 0; k < kGroupChunks; ++k) {
+                    const float d = dot8(w[i][k], x[min(k, n - 1) * 64], 0.f);
+                    acc[i] += k < n ? d : 0.f;
+                }
+                acc[i] = wave_sum(acc[i]);
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int i = 0; i < 2 * kItemRows; ++i)
+                    sh.part[((kItemRows * pr + (i >> 1)) * 2 + (i & 1)) * kMaxGroups + g] = acc[i];
+            }
+        }
+        __syncthreads();
+        done |= fresh;
+    }
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    // the reference's condition (every opcode-5 block arrived) holds by now
+    // or within a few polls: the chunk counters are added after it
+    if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    // h = bf16(h + bf16(s_j * bf16(d_j))) for j = 0, 1 in order
+    for (int r = tid; r < nrows; r += kThreads) {
+        float d0 = 0.f, d1 = 0.f;
+        for (int g = 0; g < ng; ++g) {
+            d0 += sh.part[(r * 2 + 0) * kMaxGroups + g];
+            d1 += sh.part[(r * 2 + 1) * kMaxGroups + g];
+        }
+        float h = bf2f(hpre);  // r == tid: nrows <= kThreads
+        h = rbf(h + rbf(s0 * rbf(d0)));
+        h = rbf(h + rbf(s1 * rbf(d1)));
+        st_dev16(p.hidden + row0 + r, f2bf(h));
+    }
+    drain_and_sync();
+    arrive(bar_at(p, layer, 6), 2 * (end - start));
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
+// kOverlap: the overlapped form is compiled in (the 8-expert MoE-only
+// kernel; in the others its registers would spill).
+template <bool kOverlap>
 __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                    const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
@@ -1032,6 +1292,9 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
     // here), the experts are known before the barrier, so each wave starts
     // streaming the first chunks of its first item while it waits.
     const bool known = sh.route_layer == layer;
+    if (kOverlap && p.chunk_ctr != nullptr && known && nrows <= 32 && nrows % kItemRows == 0 && (p.F % kChunkElems) == 0 &&
+        nc <= kGroupChunks * kMaxGroups)
+        return downproj_overlapped(p, sh, act, c, tim, layer, start, end);
     const int first_batch = min(nrows, kRowBatch);
     const bool early = known && wave < first_batch * 2 * S;
     RowRegs<kEarlyChunks> pre;
@@ -2377,8 +2640,8 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
                 if ((a.V & 1) && threadIdx.x == 0) a.logits[a.V - 1] = 0;
             }
         }
-        const int n = 2 * (int)gridDim.x * p.queue_len;
-        for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
+        // work-sharing cursors, then the column-chunk counters
+        for (int i = threadIdx.x; i < p.scratch_clear; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
         drain_and_sync();
         if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -2405,8 +2668,13 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
         bool ok = true;
         switch (op) {
         case 0: break;
-        case 5: ok = op_rms_router_upgate<kE, kAttn>(p, sh, act, ins, c, tim); break;
-        case 6: ok = op_expert_downproj(p, sh, act, ins, c, tim); break;
+        case 5: {
+            int consumed = 1;
+            ok = op_rms_router_upgate<kE, kAttn>(p, sh, act, ins, c, tim, consumed);
+            q += consumed - 1;
+            break;
+        }
+        case 6: ok = op_expert_downproj<kE == 8 && !kAttn>(p, sh, act, ins, c, tim); break;
         case 8: ok = op_predict<kE>(p, sh, act, ins, c, tim); break;
         case 1:
         case 2:
@@ -2802,6 +3070,8 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     if (rc != MK_OK) return rc;
 
     KParams kp{};
+    kp.chunk_ctr = nullptr;
+    kp.scratch_clear = (int32_t)(2 * (size_t)g->num_workers * (size_t)g->queue_len);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
     kp.bar = g->barriers;
@@ -2927,10 +3197,19 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
                                 : reinterpret_cast<const void *>(mk_mixtral_kernel<8, false>))
                         : (attn ? reinterpret_cast<const void *>(mk_mixtral_kernel<0, true>)
                                 : reinterpret_cast<const void *>(mk_mixtral_kernel<0, false>));
-    rc = ensure_scratch(st, kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len);
+    // scratch: exit counter, work-sharing cursors, then (overlap on) the
+    // column-chunk counters of every layer
+    const size_t cursors = 2 * (size_t)g->num_workers * (size_t)g->queue_len;
+    // compiled into the 8-expert MoE-only kernel only
+    const bool overlap = g->downproj_overlap != 0 && !g->work_sharing && g->num_experts == 8 &&
+                         g->qkv_weights == nullptr;
+    const size_t chunks = overlap ? (size_t)g->num_layers * (size_t)(g->intermediate_size / 512) : 0;
+    rc = ensure_scratch(st, kScratchSlotBase + cursors + chunks);
     if (rc != MK_OK) return rc;
 
     KParams kp;
+    kp.chunk_ctr = overlap ? st->scratch + kScratchSlotBase + cursors : nullptr;
+    kp.scratch_clear = (int32_t)(cursors + chunks);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
     kp.bar = g->barriers;

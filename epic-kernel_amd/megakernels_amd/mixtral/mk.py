@@ -46,6 +46,7 @@ def interpret_with_mk(globs: MixtralGlobals, mk_func, **launch_kwargs):
         lm_head_block_size=globs.lm_head_block_size,
         router_bias=globs.router_bias,
         predictor_weights=None if globs.predictor_weights is None else _flatten_depth(globs.predictor_weights),
+        downproj_overlap=getattr(globs, "moe_overlap", False),
         stream=(torch.cuda.current_stream(globs.hidden_states.device)
                 if globs.hidden_states.device.type == "cuda" else None),
     )

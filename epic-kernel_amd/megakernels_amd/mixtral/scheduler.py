@@ -31,6 +31,12 @@ Differences, all MI355X-motivated and recorded here:
   4 and 256 workers, 8-row blocks give every worker 24 QKV rows where 16-row
   blocks leave 32 on half of them; 4-row blocks measured slower); it stays a
   divisor of head_dim.
+* ``moe_overlap=True`` (off by default) partitions opcode 5 into one
+  instruction per block, interleaved across workers, and launches with the
+  kernel's opcode-5/6 overlap (opcode 6 starts on column chunks of the SiLU
+  output as they complete instead of after the layer's last opcode-5 block).
+  Indices, scores and barrier counts are unchanged; hidden states differ
+  only in the fp32 summation order of the down-projection rows.
 * ``make_moe_dag`` builds the MoE-only slice of one layer (optional opcode 8,
   then opcode 5 and opcode 6) for running the hot path in isolation; the
   attention prefix it skips is represented by pre-filling the O-proj barrier
@@ -131,6 +137,8 @@ def make_globals(
     down_proj_block_size: int | None = None,
     attention_partitions: str = "mi355x",
     qkv_block_size: int | None = None,
+    moe_overlap: bool = False,
+    upgate_rounds: int = 3,
 ) -> MixtralGlobals:
     """Allocate activation buffers and wrap ``model``'s stacked weights.
 
@@ -143,7 +151,9 @@ def make_globals(
     (needed when the globals live on the CPU).  ``attention_partitions``
     picks the split-KV partition policy of ``make_dag``
     (:func:`pick_num_attention_partitions`; ``"reference"`` reproduces the
-    reference's instruction list).
+    reference's instruction list).  ``moe_overlap`` selects the interleaved
+    opcode-5 partition (:func:`schedule_rms_router_upgate`) and has
+    ``interpret_with_mk`` launch with the opcode-5/6 overlap.
     """
     cfg = model.config
     device = torch.device(model.device)
@@ -229,6 +239,8 @@ def make_globals(
     )
     globs.sm_count_override = sm_count
     globs.attn_partition_policy = attention_partitions
+    globs.moe_overlap = bool(moe_overlap)
+    globs.upgate_rounds = int(upgate_rounds)
     return globs
 
 
@@ -251,7 +263,27 @@ def schedule_qkv(globs: MixtralGlobals, layer_idx: int):
 
 
 def schedule_rms_router_upgate(globs: MixtralGlobals, layer_idx: int):
+    """The reference's contiguous spans (``mkm/scheduler.py:176-196``) or,
+    with ``globs.moe_overlap``, one instruction per block in block order:
+    assigned round-robin, worker ``w`` then holds blocks ``w, w + W, ...`` as
+    consecutive queue entries (which the kernel runs as one pool), so every
+    512-row column chunk of the SiLU output is finished by many workers at
+    once and early in the stage, which is what lets opcode 6 start on it."""
     blocks = assert_div(globs.intermediate_size, globs.expert_proj_block_size)
+    if getattr(globs, "moe_overlap", False):
+        W = globs.sm_count()
+        rounds = getattr(globs, "upgate_rounds", 3)
+        if blocks % W or blocks // W < rounds:
+            return [RmsRouterUpgate(layer_idx=layer_idx, start_block_idx=b, num_blocks=1) for b in range(blocks)]
+        # `rounds` runs of contiguous blocks per worker; run r of every worker
+        # covers one contiguous span of the FFN rows
+        per = blocks // W
+        out, first = [], 0
+        for r in range(rounds):
+            n = per * (r + 1) // rounds - per * r // rounds
+            out += [RmsRouterUpgate(layer_idx=layer_idx, start_block_idx=first + w * n, num_blocks=n) for w in range(W)]
+            first += W * n
+        return out
     return [
         RmsRouterUpgate(layer_idx=layer_idx, start_block_idx=s, num_blocks=e - s)
         for s, e in _spans(blocks, globs.sm_count())

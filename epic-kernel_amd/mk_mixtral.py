@@ -34,6 +34,12 @@ sizes are the compile-time 16):
 ``reset_for_next_launch``
     the launch ends by zeroing the barrier tensor and the logits, so that
     the next launch needs no fill (neither can be read afterwards);
+``downproj_overlap``
+    opcode 5 also counts finished SiLU rows per 512-row column chunk, and
+    opcode 6 starts on groups of chunks as they complete (no counterpart in
+    the reference; ignored with ``work_sharing``); meant for an opcode-5
+    partition interleaved across workers.  Same indices, scores and barrier
+    counts; the hidden state differs only in fp32 summation order;
 ``debug_sync``
     synchronise after the launch and raise :class:`MKDeviceError` if the
     kernel recorded a failure.
@@ -63,7 +69,7 @@ __all__ = [
 _HERE = Path(__file__).resolve().parent
 _LIB_NAME = "libmk_mixtral.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 STATUS_WORDS = 16
 MAX_EXPERTS = 16
 
@@ -170,6 +176,7 @@ class MkMixtralGlobals(ctypes.Structure):
         ("argmax_out", _P),
         ("next_embed_weights", _P),
         ("reset_for_next_launch", ctypes.c_int32),
+        ("downproj_overlap", ctypes.c_int32),
     ]
 
 
@@ -323,6 +330,7 @@ def build_globals_struct(
     argmax_out=None,
     next_embed_weights=None,
     reset_for_next_launch: bool = False,
+    downproj_overlap: bool = False,
 ) -> MkMixtralGlobals:
     """Validate the reference-ordered arguments and fill the C struct.
 
@@ -436,6 +444,7 @@ def build_globals_struct(
     g.work_sharing = int(bool(work_sharing))
     g.argmax_out, g.next_embed_weights = _decode_tail(argmax_out, next_embed_weights, attn is not None, dev, H)
     g.reset_for_next_launch = int(bool(reset_for_next_launch))
+    g.downproj_overlap = int(bool(downproj_overlap))
     return g
 
 

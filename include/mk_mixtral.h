@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define MK_MIXTRAL_ABI_VERSION 3
+#define MK_MIXTRAL_ABI_VERSION 4
 #define MK_INTS_PER_INSTRUCTION 32
 #define MK_TIMING_SLOTS 128
 #define MK_STATUS_WORDS 16
@@ -217,6 +217,20 @@ typedef struct mk_mixtral_globals {
                                       and the logits are zeroed, so the next
                                       launch needs no fill; the caller then
                                       cannot read either */
+
+    /* opcode-5/6 overlap, no counterpart in the reference (its opcode 6
+     * waits for every opcode-5 block).  Nonzero, and work_sharing zero:
+     * opcode 5 also counts finished SiLU rows per 512-row chunk of F in the
+     * library's scratch, and opcode 6 starts on groups of 4 chunks as they
+     * complete, on a workgroup that routed the layer itself.  Same indices,
+     * scores and barrier counts; hidden_states differ from the zero setting
+     * only in the fp32 summation order of each row.  Pairs with an opcode-5
+     * partition whose blocks interleave across workers (worker w: blocks
+     * w, w + W, ...), which makes column chunks complete early.  Applies to
+     * MoE-only launches (qkv_weights NULL) with 8 experts; ignored
+     * otherwise.  Launches on one device must not overlap (the counters are
+     * per device). */
+    int32_t downproj_overlap;
 } mk_mixtral_globals;
 
 /* Launch one persistent-kernel pass over the instruction queues.

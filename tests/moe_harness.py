@@ -95,7 +95,8 @@ class MoECase:
 
     def __init__(self, config, seed=0, device="cuda", workers=None, ln_weight_std=None, router_bias=None,
                  predictor_sigma=None, expert_proj_block_size=None, down_proj_block_size=None,
-                 predict=False, mode="rr", generate_on_device=False, stop_after_op=None, worker_weights=None):
+                 predict=False, mode="rr", generate_on_device=False, stop_after_op=None, worker_weights=None,
+                 moe_overlap=False):
         dev = torch.device(device)
         gen_dev = dev if generate_on_device else torch.device("cpu")
         model = make_synthetic_mixtral(config, gen_dev, seed, ln_weight_std=ln_weight_std,
@@ -112,7 +113,7 @@ class MoECase:
         if workers is None:
             workers = torch.cuda.get_device_properties(dev).multi_processor_count
         kw = dict(sm_count=workers, expert_proj_block_size=expert_proj_block_size,
-                  down_proj_block_size=down_proj_block_size)
+                  down_proj_block_size=down_proj_block_size, moe_overlap=moe_overlap)
         self.g_gpu = make_globals(self.gpu_model, **kw)
         self.g_cpu = make_globals(self.cpu_model, **kw)
         nodes, end = make_moe_dag(self.g_gpu, predict=predict, stop_after_op=stop_after_op)

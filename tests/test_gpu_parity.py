@@ -169,3 +169,43 @@ def test_speed_balanced_partition(config):
     for x in draw_tokens(case.cpu_model, 3):
         case.run_token(x).assert_ok()
         case.run_token(x, work_sharing=True).assert_ok()
+
+
+@pytest.mark.parametrize("config,workers,mode,ebs", [("c1", None, "rr", None), ("c1", None, "rr", 4),
+                                                     ("c1", 64, "rr", None), ("c1", 1, "rr", None),
+                                                     ("c1", 20, "zz", None), ("c1", None, "dag", None),
+                                                     ("small", 7, "rr", None)])
+def test_moe_overlap(config, workers, mode, ebs):
+    """Interleaved opcode-5 partition (pooled instructions, per-item arrivals)
+    with opcode 6 starting on finished column groups: indices exact, hidden
+    and SiLU within tolerance, barrier tensor equal to the oracle's, over
+    consecutive launches (the chunk counters are cleared at each launch's
+    end).  C1 (F = 3584: 7 chunks) ends in a short group of 3; SMALL has 4
+    experts, so only the pooled opcode 5 applies there."""
+    cfg = C1 if config == "c1" else SMALL
+    case = MoECase(cfg, seed=21, workers=workers, mode=mode, predict=(mode == "dag"), moe_overlap=True,
+                   expert_proj_block_size=ebs)
+    for x in draw_tokens(case.cpu_model, 3):
+        res = case.run_token(x)
+        _report(f"overlap-{config}-{workers}-{mode}-{ebs}", res)
+        res.assert_ok()
+
+
+def test_moe_overlap_mixed_launches():
+    """Overlap on the reference's contiguous partition, then off, then with
+    work sharing (which turns it off), then on again: every launch matches
+    the oracle, so no launch leaves counters behind for the next."""
+    case = MoECase(C1, seed=23)
+    xs = draw_tokens(case.cpu_model, 4)
+    for x, kw in zip(xs, ({"downproj_overlap": True}, {}, {"downproj_overlap": True, "work_sharing": True},
+                          {"downproj_overlap": True})):
+        case.run_token(x, **kw).assert_ok()
+
+
+def test_moe_overlap_c2_tokens():
+    """Config 2 shapes with the overlap: a few tokens."""
+    case = MoECase(C2, seed=0, generate_on_device=True, moe_overlap=True)
+    for x in draw_tokens(case.cpu_model, 3):
+        res = case.run_token(x)
+        _report("c2-overlap", res)
+        res.assert_ok()

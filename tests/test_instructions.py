@@ -108,6 +108,45 @@ def test_partitions_use_bankers_rounding():
     assert len(schedule_rms_router_upgate(g, 0)) == 100
 
 
+def test_interleaved_upgate_partition():
+    """moe_overlap: one opcode-5 instruction per block, in block order, so a
+    round-robin assignment gives worker w blocks w, w + W, ... as
+    consecutive queue entries (the kernel's pool), and every 512-row column
+    chunk is covered by blocks of many workers."""
+    model = make_synthetic_mixtral(SMALL, "cpu", 0)
+    g = make_globals(model, sm_count=256, expert_proj_block_size=8, down_proj_block_size=16, moe_overlap=True,
+                     upgate_rounds=7)
+    assert g.moe_overlap
+    g.intermediate_size, g.hidden_size = 14336, 4096
+    ins = schedule_rms_router_upgate(g, 3)
+    assert len(ins) == 1792
+    assert [(i.layer_idx, i.start_block_idx, i.num_blocks) for i in ins[:3]] == [(3, 0, 1), (3, 1, 1), (3, 2, 1)]
+    assert [i.serialize()[:4] for i in ins[-1:]] == [[5, 3, 1791, 1]]
+    queues = round_robin_assign_to_sms(ins, 256)
+    assert [i.start_block_idx for i in queues[5]] == [5 + 256 * r for r in range(7)]
+    # chunk 0 (FFN rows 0-511, blocks 0-63) is finished by 64 different workers
+    assert len({b % 256 for b in range(64)}) == 64
+    # two rounds (the default): runs of 3 then 4 contiguous blocks per worker,
+    # round 0 covering blocks 0-767 and round 1 blocks 768-1791
+    g.upgate_rounds = 2
+    ins = schedule_rms_router_upgate(g, 0)
+    assert len(ins) == 512
+    queues = round_robin_assign_to_sms(ins, 256)
+    assert [(i.start_block_idx, i.num_blocks) for i in queues[5]] == [(15, 3), (768 + 20, 4)]
+    spans = sorted((i.start_block_idx, i.num_blocks) for i in ins)
+    assert spans[0] == (0, 3) and all(a[0] + a[1] == b[0] for a, b in zip(spans, spans[1:]))
+    assert spans[-1][0] + spans[-1][1] == 1792
+    # blocks not a multiple of the worker count: one block per instruction
+    g.intermediate_size = 3584
+    g.expert_proj_block_size = 16
+    assert len(schedule_rms_router_upgate(g, 0)) == 224
+    # the default keeps the reference's contiguous spans
+    g2 = make_globals(model, sm_count=256, expert_proj_block_size=8)
+    assert not g2.moe_overlap
+    g2.intermediate_size = 14336
+    assert len(schedule_rms_router_upgate(g2, 0)) == 256
+
+
 def test_pick_block_size():
     assert pick_block_size(14336, 256) == 8      # 1792 blocks: exactly 7 per worker
     assert pick_block_size(4096, 256) == 16      # 256 blocks: one each
