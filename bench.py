@@ -64,7 +64,8 @@ class MoEBench:
     """Per-token launches of the MoE-only schedule over resident inputs."""
 
     def __init__(self, cfg, tokens: int, seed: int = 0, router_bias=None, work_sharing: bool = False,
-                 balance: bool = False, calib_tokens: int = 16, moe_overlap: str = "off", upgate_rounds: int = 3):
+                 balance: bool = False, calib_tokens: int = 16, moe_overlap: str = "off", upgate_rounds: int = 3,
+                 balance_opcodes=(5, 6)):
         import torch
 
         import mk_mixtral
@@ -79,7 +80,12 @@ class MoEBench:
         self.model = make_synthetic_mixtral(cfg, self.dev, seed, router_bias=router_bias)
         self.residuals = make_residuals(tokens, cfg.hidden_size, generator=self.model.generator)
         # speed-balanced partitions need row-granular blocks
-        bs = dict(expert_proj_block_size=1, down_proj_block_size=1) if balance else {}
+        self.balance_opcodes = tuple(balance_opcodes)
+        bs = {}
+        if balance:
+            bs["expert_proj_block_size"] = 1
+            if 6 in self.balance_opcodes:
+                bs["down_proj_block_size"] = 1
         self.globs = g = make_globals(self.model, moe_overlap=moe_overlap in ("on", "op5"),
                                       upgate_rounds=upgate_rounds, **bs)
         nodes, end = make_moe_dag(g)
@@ -134,7 +140,7 @@ class MoEBench:
                 rates.append(worker_rates_from_timings(g.timings, g.instructions, g.expert_proj_block_size))
         self.check_status()
         self.weights = weights_from_rates(np.nanmean(np.stack(rates), axis=0))
-        self.queues = rebalance_queues(self.queues, g, self.weights)
+        self.queues = rebalance_queues(self.queues, g, self.weights, opcodes=self.balance_opcodes)
         tensorize_instructions(g, self.queues)
         s.instructions = g.instructions.data_ptr()
         s.queue_len = g.instructions.shape[1]
@@ -461,6 +467,8 @@ def main():
                          "grouped opcode 6 on the contiguous partition (op6)")
     ap.add_argument("--upgate-rounds", type=int, default=3,
                     help="c1/c2 with --moe-overlap on/op5: contiguous opcode-5 block runs per worker")
+    ap.add_argument("--balance-opcodes", default="5,6",
+                    help="with --balance: the opcodes whose rows are re-split by measured speed")
     ap.add_argument("--balance", action="store_true",
                     help="re-split rows by per-worker speed measured on a few launches (block size 1)")
     ap.add_argument("--work-sharing", action="store_true",
@@ -500,7 +508,8 @@ def main():
     print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
     overlap = args.moe_overlap
     bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
-                     moe_overlap=overlap, upgate_rounds=args.upgate_rounds)
+                     moe_overlap=overlap, upgate_rounds=args.upgate_rounds,
+                     balance_opcodes=tuple(int(x) for x in args.balance_opcodes.split(",")))
     timed = run_timed(bench, args.steps, args.warmup)
     dist = bench.per_launch_us(256)
     if args.trace:
@@ -513,7 +522,8 @@ def main():
     skewed = None
     if not args.no_skewed:
         sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
-                      moe_overlap=overlap, upgate_rounds=args.upgate_rounds, router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
+                      moe_overlap=overlap, upgate_rounds=args.upgate_rounds,
+                      balance_opcodes=tuple(int(x) for x in args.balance_opcodes.split(",")), router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
         sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
         sk_us = sk_timed["us_per_launch_events"]
         skewed = {"moe_layer_us": sk_us, "hbm_frac": nbytes / (sk_us * 1e-6) / 1e9 / HBM_PEAK_GBS,

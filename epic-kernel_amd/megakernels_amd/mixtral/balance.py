@@ -3,9 +3,12 @@
 The reference splits the FFN rows of opcode 5 and the hidden rows of opcode 6
 evenly over the workers (``megakernels/mixtral/scheduler.py:176-225``).  On
 MI355X the workers do not stream equally fast: workgroup ``w`` runs on XCD
-``w % 8``, and the workgroups on odd XCDs stream weights about 7 % slower than
-those on even XCDs (measured with the kernel's timing record; the pattern
-follows the workgroup, not the addresses it reads).  Every instruction of an
+``w % 8``, and the XCDs stream opcode-5 weights at different speeds (one
+XCD ends opcode 5 up to ~6 us after another in the kernel's timing record;
+the pattern follows the workgroup, not the addresses it reads, and varies
+between boxes).  Opcode 6, which every worker starts together after the
+barrier, ends evenly across XCDs, so ``opcodes=(5,)`` re-splits opcode 5
+only.  Every instruction of an
 opcode-5 or opcode-6 set must finish before its consumer starts, so the
 slowest worker sets the pace.
 
@@ -54,9 +57,12 @@ def weighted_spans(num_blocks: int, weights) -> list[tuple[int, int]]:
     return spans
 
 
-def rebalance_queues(queues: list[list], globs: MixtralGlobals, worker_weights) -> list[list]:
-    """Return new queues whose opcode-5 and opcode-6 instructions cover the
-    same blocks in the same order, re-split by ``worker_weights[worker]``."""
+def rebalance_queues(queues: list[list], globs: MixtralGlobals, worker_weights, opcodes=(5, 6)) -> list[list]:
+    """Return new queues whose opcode-5 and opcode-6 instructions (those
+    whose opcode is in ``opcodes``) cover the same blocks in the same order,
+    re-split by ``worker_weights[worker]``.  The weights measured on opcode 5
+    need not hold for opcode 6: all workers start it together after the
+    barrier, and its per-XCD end times are even."""
     weights = np.asarray(worker_weights, dtype=np.float64)
     if weights.shape != (len(queues),):
         raise ValueError(f"need one weight per worker ({len(queues)}), got shape {weights.shape}")
@@ -64,7 +70,7 @@ def rebalance_queues(queues: list[list], globs: MixtralGlobals, worker_weights) 
     sets: dict[tuple[int, int], list[tuple[int, int, object]]] = {}
     for w, q in enumerate(out):
         for s, ins in enumerate(q):
-            if isinstance(ins, (RmsRouterUpgate, ExpertDownProjFused)):
+            if isinstance(ins, (RmsRouterUpgate, ExpertDownProjFused)) and ins.opcode() in opcodes:
                 sets.setdefault((ins.opcode(), ins.layer_idx), []).append((w, s, ins))
     for (op, layer), members in sets.items():
         if op == RmsRouterUpgate.opcode():

@@ -72,6 +72,25 @@ def test_rebalance_keeps_cover_slots_and_barrier_totals(mode, predict):
     assert bar[0, 4, 0] == SMALL.intermediate_size and bar[0, 5, 0] == 2 * SMALL.hidden_size
 
 
+def test_rebalance_opcode5_only_leaves_opcode6():
+    """opcodes=(5,): opcode-5 rows follow the weights, opcode-6 instructions
+    stay exactly as scheduled."""
+    model, g, sched, queues = _schedule(expert_proj_block_size=1)
+    weights = np.where(np.arange(16) % 2, 0.9, 1.1)
+    new = rebalance_queues(queues, g, weights, opcodes=(5,))
+    for q_old, q_new in zip(queues, new):
+        for a, b in zip(q_old, q_new):
+            if isinstance(a, ExpertDownProjFused):
+                assert a.serialize() == b.serialize()
+    per_worker = np.zeros(16)
+    for w, q in enumerate(new):
+        for ins in q:
+            if isinstance(ins, RmsRouterUpgate):
+                per_worker[w] += ins.num_blocks
+    assert per_worker.sum() == SMALL.intermediate_size
+    assert per_worker[0::2].mean() > per_worker[1::2].mean()
+
+
 def test_rebalanced_schedule_gives_identical_oracle_results():
     model, g, sched, queues = _schedule(expert_proj_block_size=1, down_proj_block_size=1)
     new = rebalance_queues(queues, g, np.linspace(0.6, 1.4, 16))
