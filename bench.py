@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark: batch-1 Mixtral-8x7B MoE decode layer on one MI355X.
+"""Benchmark: batch-1 Mixtral-8x7B decode on one MI355X.
 
-Workload (uniform): one full-size Mixtral MoE layer
-(hidden 4096, FFN 14336, 8 experts, top-2), bf16 weights N(0, 0.02), 1024
-independent batch-1 decode tokens with residual inputs N(0, 1), all resident
-in HBM before timing.  One *step* = the 1024 tokens, each a separate launch of
-the persistent kernel (opcodes 5 and 6 over all 256 compute units), updating
-its residual in place.  ``value`` is decode tokens/s through the layer.
+Headline (the default run): Mixtral-8x7B-shaped batch-1
+greedy decode -- 32 layers, hidden 4096, 32/8 heads, 8 experts top-2 with
+FFN 14336, vocab 32000, random-init bf16 weights (94 GB, resident in HBM),
+the KV cache pre-filled to 4096 positions.  One *step* = one decode token =
+one launch of the persistent kernel over the whole model, with the argmax
+and the next token's embedding inside the launch.  ``value`` is decode
+tokens/s; ``roofline`` is the step's algorithmic bytes (weights, the K/V of
+every cached position, the LM head) over the kernel time from HIP events on
+the launch stream.
 
-Also reported: MoE-layer microseconds per launch (HIP events on the launch
-stream, averaged over the timed region, plus a per-launch median/p10/p90
-pass), the HBM roofline fraction of the layer (algorithmic bytes
-2*(E*H + H + k*3*F*H) / time / 8 TB/s), the skewed-routing variant (+2.0
-router bias on experts 0 and 1), and the CPU oracle timed on the host.
+Also in the same line:
+* ``moe_layer``: one full-size Mixtral MoE layer in isolation (BASELINE
+  config 2): 1024 batch-1 tokens per step, each a launch of opcodes 5 and 6,
+  its microseconds per launch, HBM roofline fraction of
+  2*(E*H + H + k*3*F*H) bytes, and the skewed-routing variant (+2.0 router
+  bias on experts 0 and 1);
+* ``cpu_baseline``: the CPU oracle (a restatement of the reference's
+  python_vm) timed on the host over a bounded slice of the same decode
+  workload and scaled to tokens/s.
 
-``python bench.py --gpus 1 --steps 10 --warmup 2``
+``python bench.py`` (defaults: 128 timed steps after 2 warmup steps);
+``--config c2`` / ``c1`` run the MoE layer alone, ``c3`` / ``c5`` the other
+decode configs.
 """
 
 from __future__ import annotations
@@ -41,6 +50,7 @@ HBM_PEAK_GBS = 8000.0
 # reads for a device copy of known size (FETCH x 2.0, WRITE x 1.0); the
 # counter runs are summarised under profiles/.
 MEASURED_TRAFFIC_BYTES = {"c2": 708_573_701}
+TRAFFIC_UNIT = "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
 
 
 def moe_layer_bytes(cfg) -> int:
@@ -258,27 +268,26 @@ def decode_bytes_per_token_llama(cfg, seq_len: int) -> int:
     return 2 * (L * (attn + mlp + kv) + V * H + H)
 
 
-def decode_bench(args):
+def decode_bench(args, config: str, steps: int, warmup: int):
     """Whole-model greedy decode through MK_Generator
     (Llama-3.2-3B shape, 2048 cached positions, dense VM) and configs 4 and 5
     (Mixtral-8x7B shape, 4096 / 16384 cached positions).  Random-init weights
     resident in HBM, a KV cache pre-filled with N(0, 1) to the context
-    length, `decode_steps` timed steps after `warmup` untimed ones."""
+    length, `steps` timed steps after `warmup` untimed ones.  Returns the
+    bench line (a dict) and the model."""
     import torch
 
     from megakernels_amd.mixtral.generate import MK_Generator
     from megakernels_amd.mixtral.synthetic import C4, make_synthetic_mixtral
 
-    llama = args.config == "c3"
+    llama = config == "c3"
     if llama:
         from megakernels_amd.latency.synthetic import C3, make_synthetic_llama
 
         cfg, prefill = C3, 2048
     else:
-        cfg, prefill = C4, (4096 if args.config == "c4" else 16384)
-    steps = args.decode_steps or (256 if llama else 128)
-    warmup = max(1, args.warmup)
-    print(f"bench: building {args.config} ({cfg.num_hidden_layers} layers, {prefill} cached positions) on cuda:0",
+        cfg, prefill = C4, (4096 if config == "c4" else 16384)
+    print(f"bench: building {config} ({cfg.num_hidden_layers} layers, {prefill} cached positions) on cuda:0",
           file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     if llama:
@@ -300,9 +309,12 @@ def decode_bench(args):
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
+    gpu_s = gen.last_gpu_seconds
     import mk_mixtral
 
     mk_mixtral.raise_if_failed("cuda")
+    print(f"bench: {config} {steps / secs:.1f} tokens/s ({secs / steps * 1e3:.3f} ms per step, "
+          f"{gpu_s / steps * 1e3:.3f} ms by HIP events)", file=sys.stderr, flush=True)
     if args.trace:
         from megakernels_amd.trace import TimingRecord, format_report, save_record
 
@@ -317,8 +329,10 @@ def decode_bench(args):
         print(format_report(rec), file=sys.stderr, flush=True)
     ms = secs / steps * 1e3
     nbytes = (decode_bytes_per_token_llama if llama else decode_bytes_per_token)(cfg, prefill + steps // 2)
-    achieved = nbytes / (ms * 1e-3) / 1e9
+    kernel_s = gpu_s / steps
+    achieved = nbytes / kernel_s / 1e9
     g = gen.schedule.globs
+    kernel = "mk_llama_kernel" if llama else "mk_mixtral_kernel<8, true>"
     out = {
         "metric": METRIC,
         "value": steps / secs,
@@ -331,14 +345,15 @@ def decode_bench(args):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
+        "data": "synthetic (random-init weights N(0, 0.02), KV cache N(0, 1))",
         "config": {
             "workload": (f"BASELINE config 3: Llama-3.2-3B-shaped batch-1 greedy decode (28 layers, hidden 3072, "
                          f"24/8 heads, head dim 128, FFN 8192, vocab 128256, RoPE theta 500000), KV cache pre-filled "
                          f"to {prefill} positions, one persistent-kernel launch per token (dense VM)" if llama else
-                         f"BASELINE config {'4' if args.config == 'c4' else '5'}: Mixtral-8x7B-shaped batch-1 greedy "
-                         f"decode (32 layers, 32/8 heads, head dim 128, 8 experts top-2, vocab 32000), KV cache "
-                         f"pre-filled to {prefill} positions, one persistent-kernel launch per token"),
+                         f"BASELINE config {'4' if config == 'c4' else '5'}: Mixtral-8x7B-shaped batch-1 greedy "
+                         f"decode (32 layers, hidden 4096, 32/8 heads, head dim 128, 8 experts top-2 with FFN 14336, "
+                         f"vocab 32000, RoPE theta 1e6), KV cache pre-filled to {prefill} positions, one "
+                         f"persistent-kernel launch per token"),
             "prefill": prefill,
             "workers": g.sm_count(),
             "attention_partitions": int(max(i.num_partials for i in gen.schedule.get_linear_instructions()
@@ -347,30 +362,164 @@ def decode_bench(args):
             "predictor": None if llama else not args.no_predict,
             "assignment": args.assign,
             "qkv_block_size": g.qkv_block_size,
-            "block_sizes": {k: getattr(g, k) for k in ("up_gate_proj_block_size", "down_proj_block_size",
-                                                       "matvec_reduction_size") if hasattr(g, k)},
+            "block_sizes": {k: getattr(g, k) for k in ("up_gate_proj_block_size", "expert_proj_block_size",
+                                                       "down_proj_block_size", "matvec_reduction_size")
+                            if hasattr(g, k)},
             "partition_policy": args.partitions,
             "argmax": "torch, between launches" if args.host_argmax else "in-kernel, with the next embedding",
             "fills_between_launches": args.host_argmax or args.no_reset,
         },
+        "ms_per_step_hip_events": kernel_s * 1e3,
         "roofline": {
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES.get(config),
+            "traffic_unit": TRAFFIC_UNIT,
             "bytes_per_launch": nbytes,
-            "kernel": "mk_llama_kernel (whole model)" if llama else "mk_mixtral_kernel (whole model)",
+            "bytes_per_launch_is": "weights of every layer (attention, norms, router, the two selected experts), "
+                                   "K and V of every cached position at the mean context of the timed steps, "
+                                   "LM head",
+            "kernel": kernel,
+            "kernel_time": "HIP events on the launch stream over the timed steps, per step",
         },
         "tokens_tail": tokens[0, -8:].tolist(),
     }
-    print(json.dumps(out), flush=True)
+    return out, model, gen
 
 
-def cpu_baseline(bench, seconds: float, threads: int):
+def cpu_baseline_decode(model, prefill: int, seconds: float, threads: int, sm_count: int, layers: int = 2):
+    """The CPU oracle (restated python_vm: C + OpenMP matvecs, torch CPU
+    attention) on a bounded slice of the config-4 decode step: the first
+    ``layers`` layers of the same model with the LM head, at the same cached
+    context, stepped until ``seconds`` have passed.  The per-layer time and
+    the LM head's time are measured separately and scaled to a whole step
+    of all L layers: tokens/s = 1 / (L * t_layer + t_lm_head)."""
+    import torch
+
+    from megakernels_amd.mixtral.scheduler import make_dag, make_globals
+    from megakernels_amd.mixtral.synthetic import slice_layers
+    from megakernels_amd.scheduler import Schedule
+    from oracle import python_vm as oracle
+
+    oracle.set_num_threads(threads)
+    torch.set_num_threads(threads)
+    L = model.config.num_hidden_layers
+    cpu = slice_layers(model, layers, "cpu")
+    g = make_globals(cpu, seq_len=prefill, sm_count=sm_count)
+    g.pos_id = prefill
+    nodes, end = make_dag(g)
+    linear = Schedule(g, nodes, end).get_linear_instructions()
+    t_layers = t_head = 0.0
+    steps = 0
+    t0 = time.perf_counter()
+    while steps == 0 or time.perf_counter() - t0 < seconds:
+        g.hidden_states.copy_(cpu.embed_tokens[1 + steps])
+        g.barriers.zero_()
+        g.logits.zero_()
+        for ins in linear:
+            t1 = time.perf_counter()
+            oracle.INSTRUCTION_TO_SOLVER[type(ins)](g, ins)
+            dt = time.perf_counter() - t1
+            if ins.opcode() == 7:
+                t_head += dt
+            else:
+                t_layers += dt
+        steps += 1
+    elapsed = time.perf_counter() - t0
+    per_layer = t_layers / steps / layers
+    head = t_head / steps
+    token_s = L * per_layer + head
+    return {
+        "value": 1.0 / token_s,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} decode steps of layers 0-{layers - 1} of the same config-4 model with its LM head, "
+                  f"{prefill} cached positions, through the oracle python_vm restatement ({len(linear)} "
+                  f"instructions per step, C+OpenMP matvecs and torch CPU attention), {elapsed:.1f} s; "
+                  f"per token = {L} x {per_layer * 1e3:.1f} ms per layer + {head * 1e3:.1f} ms LM head",
+        "ms_per_layer": per_layer * 1e3,
+        "ms_lm_head": head * 1e3,
+        "cpu_model": cpu_model_name(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def layer_bench(args, config: str, steps: int, warmup: int):
+    """One MoE layer per launch (config 2 or 1), uniform and skewed; returns
+    the figures and the uniform bench object."""
+    import torch
+
+    from megakernels_amd.mixtral.synthetic import C1, C2
+
+    cfg = C2 if config == "c2" else C1
+    print(f"bench: building {config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
+    overlap = args.moe_overlap
+    bal = tuple(int(x) for x in args.balance_opcodes.split(","))
+    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
+                     moe_overlap=overlap, upgate_rounds=args.upgate_rounds, balance_opcodes=bal)
+    timed = run_timed(bench, steps, warmup)
+    dist = bench.per_launch_us(256)
+    if args.trace and config != "c4":
+        record_trace(bench, args.trace)
+    nbytes = moe_layer_bytes(cfg)
+    us = timed["us_per_launch_events"]
+    achieved = nbytes / (us * 1e-6) / 1e9
+    print(f"bench: {config} uniform {us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+    skewed = None
+    if not args.no_skewed:
+        sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
+                      moe_overlap=overlap, upgate_rounds=args.upgate_rounds, balance_opcodes=bal,
+                      router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
+        sk_timed = run_timed(sk, max(1, steps // 2), 1)
+        sk_us = sk_timed["us_per_launch_events"]
+        skewed = {"moe_layer_us": sk_us, "hbm_frac": nbytes / (sk_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                  "router_bias": "+2.0 on experts 0 and 1"}
+        del sk
+        torch.cuda.empty_cache()
+        print(f"bench: {config} skewed {sk_us:.2f} us/launch", file=sys.stderr, flush=True)
+    g = bench.globs
+    fig = {
+        "workload": f"BASELINE config {'2' if config == 'c2' else '1'}: one Mixtral-8x7B-shaped MoE layer (hidden "
+                    f"{cfg.hidden_size}, FFN {cfg.intermediate_size}, {cfg.num_local_experts} experts, "
+                    f"top-{cfg.num_experts_per_tok}), {bench.tokens} batch-1 tokens per step with residuals N(0, 1), "
+                    "one persistent-kernel launch (opcodes 5 and 6) per token",
+        "steps": steps,
+        "ms_per_step": timed["wall_s"] / steps * 1e3,
+        "tokens_per_step": bench.tokens,
+        "workers": g.sm_count(),
+        "expert_proj_block_size": g.expert_proj_block_size,
+        "down_proj_block_size": g.down_proj_block_size,
+        "work_sharing": args.work_sharing,
+        "speed_balanced_partition": args.balance,
+        "moe_overlap": overlap,
+        "moe_layer_us": us,
+        "moe_layer_us_per_launch": dist,
+        "hbm_frac": achieved / HBM_PEAK_GBS,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": MEASURED_TRAFFIC_BYTES.get(config),
+            "traffic_unit": TRAFFIC_UNIT,
+            "bytes_per_launch": nbytes,
+            "kernel": "mk_mixtral_kernel<8, false>",
+            "kernel_time": "HIP events on the launch stream over the timed steps, per launch",
+        },
+        "skewed": skewed,
+    }
+    return fig, bench, timed
+
+
+def cpu_baseline_layer(bench, seconds: float, threads: int):
     """The CPU oracle (restated python_vm, C + OpenMP) on the same weights,
-    inputs and instruction list, over a bounded sample of tokens."""
+    inputs and instruction list as the MoE-layer bench, over a bounded sample
+    of tokens."""
     import torch
 
     from megakernels_amd.mixtral.scheduler import make_globals, prefill_oproj_barrier
@@ -412,7 +561,7 @@ def cpu_baseline(bench, seconds: float, threads: int):
         agree += int(torch.equal(sel[t].cpu(), g.selected_expert_indices))
     return {
         "value": done / elapsed,
-        "unit": "tokens/s",
+        "unit": "MoE-layer tokens/s",
         "cores": oracle.get_num_threads(),
         "kind": "port",
         "sample": f"{done} config-2 tokens through the oracle python_vm restatement (opcodes 5+6, "
@@ -427,15 +576,21 @@ def cpu_baseline(bench, seconds: float, threads: int):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=0,
+                    help="timed steps (default: 128 decode steps for c4/c5, 256 for c3 as BASELINE states them; "
+                         "10 steps of --tokens launches for c1/c2)")
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--tokens", type=int, default=1024)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
-                    help="c1/c2: one MoE layer per launch (c2 is the headline); c3: whole-model greedy decode of "
-                         "the Llama-3.2-3B shape (2048 cached positions); c4/c5: whole-model greedy decode of the "
-                         "Mixtral-8x7B shape with 4096 / 16384 cached positions")
-    ap.add_argument("--decode-steps", type=int, default=0,
-                    help="timed decode steps (default: 256 for c3, 128 for c4/c5, as BASELINE states them)")
+    ap.add_argument("--tokens", type=int, default=1024, help="c1/c2 (and the headline's layer figures): tokens "
+                                                             "per step")
+    ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c4 (default): whole-model greedy decode of the Mixtral-8x7B shape with 4096 cached "
+                         "positions, plus the config-2 MoE layer figures and the CPU baseline; c5: the same with "
+                         "16384 cached positions; c3: the Llama-3.2-3B shape (2048 cached positions, dense VM); "
+                         "c1/c2: one MoE layer per launch alone")
+    ap.add_argument("--decode-steps", type=int, default=0, help="alias of --steps for c3/c4/c5")
+    ap.add_argument("--layer-steps", type=int, default=10,
+                    help="c4: timed steps (of --tokens launches) of the config-2 layer figures")
+    ap.add_argument("--no-layer", action="store_true", help="c4: leave out the config-2 layer figures")
     ap.add_argument("--assign", default="rr", choices=["rr", "zz", "wave", "dag"],
                     help="c3/c4/c5: instruction-to-worker assignment of the whole-model schedule")
     ap.add_argument("--qkv-block", type=int, default=0,
@@ -444,10 +599,10 @@ def main():
                     help="c3/c4/c5: split-KV partition policy: mi355x, mi355x:N (at most N partitions per KV head) "
                          "or reference")
     ap.add_argument("--block-size", action="append", default=[], metavar="NAME=N",
-                    help="c3: override a dense-VM block size (up_gate_proj_block_size, down_proj_block_size, "
-                         "o_proj_block_size, lm_head_block_size, matvec_reduction_size)")
+                    help="c3/c4/c5: override a block size of make_globals (e.g. up_gate_proj_block_size, "
+                         "down_proj_block_size, o_proj_block_size, lm_head_block_size, matvec_reduction_size)")
     ap.add_argument("--no-predict", action="store_true",
-                    help="c4/c5: leave opcode 8 (expert prediction) and the early expert loads that use it out")
+                    help="c4/c5: leave out opcode 8 (expert prediction) and the early expert loads that use it")
     ap.add_argument("--predict-sigma", type=float, default=None,
                     help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
     ap.add_argument("--host-argmax", action="store_true",
@@ -474,8 +629,8 @@ def main():
     ap.add_argument("--work-sharing", action="store_true",
                     help="idle workers take unclaimed opcode-5 rows of other workers")
     ap.add_argument("--trace", default="", metavar="NPZ",
-                    help="after the timed run, record the kernel's timing slots for 8 launches, save the "
-                         "last as NPZ and print the trace analysis to stderr")
+                    help="after the timed run, record the kernel's timing slots (8 launches for c1/c2, one decode "
+                         "step for c3/c4/c5), save the last as NPZ and print the trace analysis to stderr")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (reads MIB, writes MIB) and exit; "
                          "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -498,88 +653,54 @@ def main():
         print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
         return
 
-    from megakernels_amd.mixtral.synthetic import C1, C2
-
+    threads = args.cpu_threads or os.cpu_count()
+    warmup = max(1, args.warmup)
     if args.config in ("c3", "c4", "c5"):
-        decode_bench(args)
+        steps = args.steps or args.decode_steps or (256 if args.config == "c3" else 128)
+        out, model, gen = decode_bench(args, args.config, steps, warmup)
+        if args.config == "c4" and not args.no_cpu:
+            print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)", file=sys.stderr,
+                  flush=True)
+            out["cpu_baseline"] = cpu_baseline_decode(model, out["config"]["prefill"], args.cpu_seconds, threads,
+                                                      gen.schedule.globs.sm_count())
+        del model, gen
+        torch.cuda.empty_cache()
+        if args.config == "c4" and not args.no_layer:
+            fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
+            out["moe_layer"] = fig
+            del bench
+            torch.cuda.empty_cache()
+        print(json.dumps(out), flush=True)
         return
 
-    cfg = C2 if args.config == "c2" else C1
-    print(f"bench: building {args.config} weights and {args.tokens} tokens on cuda:0", file=sys.stderr, flush=True)
-    overlap = args.moe_overlap
-    bench = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
-                     moe_overlap=overlap, upgate_rounds=args.upgate_rounds,
-                     balance_opcodes=tuple(int(x) for x in args.balance_opcodes.split(",")))
-    timed = run_timed(bench, args.steps, args.warmup)
-    dist = bench.per_launch_us(256)
-    if args.trace:
-        record_trace(bench, args.trace)
-    nbytes = moe_layer_bytes(cfg)
-    us = timed["us_per_launch_events"]
-    achieved = nbytes / (us * 1e-6) / 1e9
-    print(f"bench: uniform {us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
-
-    skewed = None
-    if not args.no_skewed:
-        sk = MoEBench(cfg, args.tokens, seed=0, work_sharing=args.work_sharing, balance=args.balance,
-                      moe_overlap=overlap, upgate_rounds=args.upgate_rounds,
-                      balance_opcodes=tuple(int(x) for x in args.balance_opcodes.split(",")), router_bias=[2.0, 2.0] + [0.0] * (cfg.num_local_experts - 2))
-        sk_timed = run_timed(sk, max(1, args.steps // 2), 1)
-        sk_us = sk_timed["us_per_launch_events"]
-        skewed = {"moe_layer_us": sk_us, "hbm_frac": nbytes / (sk_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                  "router_bias": "+2.0 on experts 0 and 1"}
-        del sk
-        torch.cuda.empty_cache()
-        print(f"bench: skewed {sk_us:.2f} us/launch", file=sys.stderr, flush=True)
-
+    steps = args.steps or 10
+    fig, bench, timed = layer_bench(args, args.config, steps, args.warmup)
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or os.cpu_count()
-        print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(bench, args.cpu_seconds, threads)
-
-    g = bench.globs
+        print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)", file=sys.stderr,
+              flush=True)
+        cpu = cpu_baseline_layer(bench, args.cpu_seconds, threads)
     out = {
         "metric": METRIC,
-        "value": bench.tokens * args.steps / timed["wall_s"],
-        "unit": "tokens/s",
+        "value": bench.tokens * steps / timed["wall_s"],
+        "unit": "MoE-layer tokens/s (one layer per launch, not whole-model decode)",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": timed["wall_s"] / args.steps * 1e3,
+        "ms_per_step": timed["wall_s"] / steps * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": f"BASELINE config {'2' if args.config == 'c2' else '1'} uniform: one Mixtral-8x7B-shaped "
-                        f"MoE layer (hidden {cfg.hidden_size}, FFN {cfg.intermediate_size}, "
-                        f"{cfg.num_local_experts} experts, top-{cfg.num_experts_per_tok}), {bench.tokens} "
-                        "batch-1 decode tokens per step, one persistent-kernel launch per token",
-            "tokens_per_step": bench.tokens,
-            "workers": g.sm_count(),
-            "expert_proj_block_size": g.expert_proj_block_size,
-            "down_proj_block_size": g.down_proj_block_size,
-            "work_sharing": args.work_sharing,
-            "speed_balanced_partition": args.balance,
-            "moe_overlap": overlap,
-        },
-        "moe_layer_us": us,
-        "moe_layer_us_per_launch": dist,
-        "hbm_frac": achieved / HBM_PEAK_GBS,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
-            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-            "bytes_per_launch": nbytes,
-            "kernel": "mk_mixtral_kernel",
-        },
-        "skewed": skewed,
+        "data": "synthetic (random-init weights N(0, 0.02), residuals N(0, 1))",
+        "config": {k: fig[k] for k in ("workload", "tokens_per_step", "workers", "expert_proj_block_size",
+                                       "down_proj_block_size", "work_sharing", "speed_balanced_partition",
+                                       "moe_overlap")},
+        "moe_layer_us": fig["moe_layer_us"],
+        "moe_layer_us_per_launch": fig["moe_layer_us_per_launch"],
+        "hbm_frac": fig["hbm_frac"],
+        "roofline": fig["roofline"],
+        "skewed": fig["skewed"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

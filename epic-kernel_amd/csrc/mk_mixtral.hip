@@ -53,9 +53,6 @@
 #ifndef MK_NT_LOADS
 #define MK_NT_LOADS 1
 #endif
-#ifndef MK_DOT2_BUILTIN
-#define MK_DOT2_BUILTIN 0
-#endif
 // Work sharing (opcode 5): the last MK_TAIL_ITEMS items of every opcode-5
 // instruction are claimed through a cursor in HBM, so the other workers of
 // its group (MK_POOL_GROUP consecutive workers, which sit on different XCDs)
@@ -132,7 +129,25 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(4))) int32_t ins_t;
 typedef __attribute__((address_space(3))) void lds_void_t;          // LDS pointer (global_load_lds destination)
 typedef const __attribute__((address_space(1))) void global_void_t;  // global pointer (global_load_lds source)
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Parameters of the attention opcodes (1-4) and the LM head (7).  They sit
+// in the kernel's argument block (KParams::attn_params), one copy per
+// launch, and are read through the constant address space like the
+// instruction words: the kernel never writes them, so the reads are scalar
+// loads (cached, and not queued behind the wave's outstanding weight loads
+// as vector loads would be), and the opcode-5/6 loops keep none of them in
+// registers.
+struct AttnParams {
+    const uint16_t *qkv, *attn_ln, *oproj, *lm_norm, *lm_head;
+    uint16_t *kc, *vc, *q_rope, *attn_out, *logits;
+    const float *rope_cos, *rope_sin;
+    float *lse_int, *out_int;
+    int32_t Hq, Hkv, D, V, T, P;
+    int32_t qkv_bs, kv_bs, lm_bs, lm_red;
+    float attn_scale;
+    int32_t skip_red;
+    int32_t kv_ring;  // opcode-2 LDS ring chunks (kAttnSub or kKvRingMax)
+};
 
 struct KParams {
     const int32_t *instructions;
@@ -160,11 +175,8 @@ struct KParams {
     uint32_t timeout_ticks;
     int32_t *scratch;
     int32_t work_sharing;
-    // attention side and LM head (opcodes 1-4, 7): attn == 0 when absent,
-    // else `ap` points at their parameters in device memory (read only by
-    // those opcodes, so the opcode-5/6 loops carry none of them)
+    // attention side and LM head (opcodes 1-4, 7): attn == 0 when absent
     int32_t attn;
-    const struct AttnParams *ap;
     uint32_t pos;  // pos_id: changes every decode step, so it stays a kernel argument
     // arrivals on [l][5][0] that complete a layer's down-projection (Mixtral:
     // 2 * H / down_bs; dense Llama: (F / red_cols) * (H / down_bs))
@@ -189,26 +201,17 @@ struct KParams {
     // that are complete instead of waiting for the whole layer
     int32_t *chunk_ctr;
     int32_t scratch_clear;  // scratch ints from kScratchSlotBase the last workgroup zeroes
+    AttnParams attn_params;  // read only through attn_of()
 };
 
-struct AttnParams {
-    const uint16_t *qkv, *attn_ln, *oproj, *lm_norm, *lm_head;
-    uint16_t *kc, *vc, *q_rope, *attn_out, *logits;
-    const float *rope_cos, *rope_sin;
-    float *lse_int, *out_int;
-    int32_t Hq, Hkv, D, V, T, P;
-    int32_t qkv_bs, kv_bs, lm_bs, lm_red;
-    float attn_scale;
-    int32_t skip_red;
-    int32_t kv_ring;  // opcode-2 LDS ring chunks (kAttnSub or kKvRingMax)
-};
-
-// The attention parameters are read through the constant address space,
-// like the instruction words: the host writes them before the launch and the
-// kernel never does, so the reads are scalar loads (cached, and not queued
-// behind the wave's outstanding weight loads as vector loads would be).
+// The launch's attention parameters, addressed in the kernel-argument
+// segment itself (KParams is the kernel's only argument, at offset 0).
 typedef const __attribute__((address_space(4))) AttnParams attn_c;
-__device__ __forceinline__ attn_c &attn_of(const KParams &p) { return *(attn_c *)(p.ap); }
+__device__ __forceinline__ attn_c &attn_of(const KParams &) {
+    const __attribute__((address_space(4))) char *kernarg =
+        (const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr();
+    return *reinterpret_cast<attn_c *>(kernarg + offsetof(KParams, attn_params));
+}
 
 // Per-workgroup state that outlives a single instruction.
 struct SharedState {
@@ -302,17 +305,10 @@ __device__ __forceinline__ float dot2_fma(uint32_t w, uint32_t a, float acc) {
 }
 
 __device__ __forceinline__ float dot8(u32x4 w, u32x4 a, float acc) {
-#if MK_DOT2_BUILTIN
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.x), __builtin_bit_cast(bf16x2, a.x), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.y), __builtin_bit_cast(bf16x2, a.y), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.z), __builtin_bit_cast(bf16x2, a.z), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.w), __builtin_bit_cast(bf16x2, a.w), acc, false);
-#else
     acc = dot2_fma(w.x, a.x, acc);
     acc = dot2_fma(w.y, a.y, acc);
     acc = dot2_fma(w.z, a.z, acc);
     acc = dot2_fma(w.w, a.w, acc);
-#endif
     return acc;
 }
 
@@ -910,6 +906,15 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
             }
             sh.grp_first[K] = first;
         }
+    } else if (threadIdx.x == 0) {
+        // work sharing: a pool of this instruction alone, which the static
+        // path below uses when the group has more instructions than the
+        // shared pool can list
+        sh.grp_row0[0] = start * p.expert_bs;
+        sh.grp_nrows[0] = nb * p.expert_bs;
+        sh.grp_first[0] = 0;
+        sh.grp_first[1] = 2 * nb * p.expert_bs;
+        sh.grp_done[0] = 0;
     }
     consumed = K;
     RouterRegs<kE> rr;
@@ -991,8 +996,9 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
             st_dev16(p.sel_score, sc0);
             st_dev16(p.sel_score + 1, sc1);
         }
-        // pooled instructions arrive one by one: publish before any of them
-        if (!p.work_sharing) drain_and_sync();
+        // items complete (and arrive) one wave at a time, and a wave may do
+        // none: every wave's part of the publication completes first
+        drain_and_sync();
     }
     stamp(tim, MK_TEVENT_FIRST_LOAD);
 
@@ -1055,11 +1061,15 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
         upgate_item_done(p, sh, layer, pending, lane);
         drain_and_sync();
         stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
-        // the pooled slots share this one's times
+        // the pooled slots share this one's times (one stream of items over
+        // the same window, so each slot's bytes are spread over it)
         if (tim != nullptr && threadIdx.x == 0)
             for (int m = 1; m < K; ++m) {
-                tim[m * MK_TIMING_SLOTS + MK_TEVENT_START] = tim[MK_TEVENT_START];
-                tim[m * MK_TIMING_SLOTS + MK_TEVENT_END] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
+                int32_t *tm = tim + m * MK_TIMING_SLOTS;
+                for (const int ev : {MK_TEVENT_START, MK_TEVENT_AT_GMEM_WAIT, MK_TEVENT_DONE_GMEM_WAIT,
+                                     MK_TEVENT_FIRST_LOAD, MK_TEVENT_DONE_GMEM_STORE})
+                    tm[ev] = tim[ev];
+                tm[MK_TEVENT_END] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
             }
     }
     return true;
@@ -2629,12 +2639,12 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
     }
     __syncthreads();
     if (sh.flag) {
-        if (p.argmax_out != nullptr && p.ap != nullptr && !aborted(p)) exit_argmax(p, sh);
+        if (p.argmax_out != nullptr && p.attn && !aborted(p)) exit_argmax(p, sh);
         if (p.reset_next > 0) {
             // every other workgroup is done with the barriers, and the
             // argmax above has read the logits
             zero_words(reinterpret_cast<uint32_t *>(p.bar), (size_t)p.num_layers * p.bar_ops * p.bar_width);
-            if (p.reset_next > 1 && p.ap != nullptr) {
+            if (p.reset_next > 1 && p.attn) {
                 attn_c &a = attn_of(p);
                 zero_words(reinterpret_cast<uint32_t *>(a.logits), (size_t)(a.V >> 1));
                 if ((a.V & 1) && threadIdx.x == 0) a.logits[a.V - 1] = 0;
@@ -2750,6 +2760,14 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
 
 constexpr int kMaxDevices = 64;
 
+// Library state per device.  The scratch buffer (exit counter, work-sharing
+// cursors, column-chunk counters) and the status words are shared by every
+// launch on the device, and a persistent kernel needs all of its workgroups
+// resident at once, which two of them running together on one device cannot
+// be promised.  So launches on one device run one after another: a launch on
+// a stream other than the previous launch's first makes its stream wait for
+// everything the previous one has queued (launch_mutex keeps the check, the
+// scratch buffer and the launch together).
 struct DeviceState {
     bool ready = false;
     int num_cus = 0;
@@ -2757,8 +2775,10 @@ struct DeviceState {
     int32_t *status = nullptr;
     int32_t *scratch = nullptr;
     size_t scratch_ints = 0;
-    AttnParams *attn = nullptr;  // attention parameters of the launches that have them
-    AttnParams attn_host{};      // what `attn` holds (after the stream reaches the copy)
+    std::mutex launch_mutex;
+    bool launched = false;
+    hipStream_t last_stream = nullptr;
+    hipEvent_t order_event = nullptr;
 };
 
 std::mutex g_mutex;
@@ -2831,39 +2851,49 @@ int ensure_scratch(DeviceState *st, size_t need) {
     return MK_OK;
 }
 
-// The device copy of the attention parameters, refreshed only when they
-// change (a decode loop launches the same tensors every step); the copy is
-// stream-ordered after the launches that read the previous contents.
-int upload_attn(DeviceState *st, const AttnParams &a, hipStream_t stream, const AttnParams **out) {
+// Co-residency check, then the launch of `fn` (a persistent kernel over
+// `workers` workgroups).
+// Orders a launch on `stream` after the device's previous launch (the
+// caller holds st->launch_mutex): same stream, nothing to do; another
+// stream waits on an event recorded on the previous one now, which follows
+// all the work queued there.  If that stream no longer exists (recording
+// fails), its work has been handed to the device already, and a device
+// synchronisation covers it.
+int order_after_previous(DeviceState *st, hipStream_t stream) {
+    if (!st->launched || st->last_stream == stream) return MK_OK;
     hipError_t e;
-    if (st->attn == nullptr) {
-        std::lock_guard<std::mutex> lock(g_mutex);
-        if (st->attn == nullptr &&
-            (e = hipMalloc(reinterpret_cast<void **>(&st->attn), sizeof(AttnParams))) != hipSuccess)
-            return hip_fail(e, "hipMalloc");
+    if (st->order_event == nullptr &&
+        (e = hipEventCreateWithFlags(&st->order_event, hipEventDisableTiming)) != hipSuccess)
+        return hip_fail(e, "hipEventCreateWithFlags");
+    e = hipEventRecord(st->order_event, st->last_stream);
+    if (e == hipSuccess) {
+        e = hipStreamWaitEvent(stream, st->order_event, 0);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+        return MK_OK;
     }
-    if (std::memcmp(&a, &st->attn_host, sizeof(a)) != 0) {
-        if ((e = hipMemcpyAsync(st->attn, &a, sizeof(a), hipMemcpyHostToDevice, stream)) != hipSuccess)
-            return hip_fail(e, "hipMemcpyAsync");
-        st->attn_host = a;
-    }
-    *out = st->attn;
+    (void)hipGetLastError();
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
     return MK_OK;
 }
 
-// Co-residency check, then the launch of `fn` (a persistent kernel over
-// `workers` workgroups).
+// Co-residency check, ordering after the device's previous launch, then the
+// launch of `fn` (a persistent kernel over `workers` workgroups).  The
+// caller holds st->launch_mutex.
 int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t lds, KParams &kp,
                       hipStream_t stream) {
     int blocks = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds);
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
+    const int rc = order_after_previous(st, stream);
+    if (rc != MK_OK) return rc;
     void *args[] = {&kp};
     e = hipLaunchKernel(fn, dim3((unsigned)workers), dim3(kThreads), args, lds, stream);
     if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel");
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "hipGetLastError");
+    st->launched = true;
+    st->last_stream = stream;
     return MK_OK;
 }
 
@@ -3054,6 +3084,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     DeviceState *st = nullptr;
     rc = device_state(dev, &st);
     if (rc != MK_OK) return rc;
+    std::lock_guard<std::mutex> launch_lock(st->launch_mutex);
     const int kv_ring = kv_ring_llama(g, (size_t)st->max_lds);
     if (kv_ring < 1) return MK_ERR_UNSUPPORTED;
     size_t lds = lds_bytes_llama(g, kv_ring);
@@ -3134,8 +3165,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     a.attn_scale = g->attn_scale;
     a.skip_red = g->skip_attn_reduction ? 1 : 0;
     a.kv_ring = kv_ring;
-    rc = upload_attn(st, a, reinterpret_cast<hipStream_t>(stream), &kp.ap);
-    if (rc != MK_OK) return rc;
+    kp.attn_params = a;
     kp.pos = g->pos_id;
     return launch_persistent(reinterpret_cast<const void *>(mk_llama_kernel), st, g->num_workers, lds, kp,
                              reinterpret_cast<hipStream_t>(stream));
@@ -3186,6 +3216,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     DeviceState *st = nullptr;
     rc = device_state(dev, &st);
     if (rc != MK_OK) return rc;
+    std::lock_guard<std::mutex> launch_lock(st->launch_mutex);
 
     const int kv_ring = kv_ring_for(g, (size_t)st->max_lds);
     if (kv_ring < 1) return MK_ERR_UNSUPPORTED;
@@ -3250,7 +3281,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.next_embed = g->next_embed_weights;
     kp.reset_next = g->reset_for_next_launch ? (g->qkv_weights != nullptr ? 2 : 1) : 0;
     kp.attn = g->qkv_weights != nullptr;
-    kp.ap = nullptr;
+    kp.attn_params = AttnParams{};
     if (kp.attn) {
         AttnParams a{};
         a.qkv = g->qkv_weights;
@@ -3280,8 +3311,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
         a.attn_scale = g->attn_scale;
         a.skip_red = g->skip_attn_reduction ? 1 : 0;
         a.kv_ring = kv_ring;
-        rc = upload_attn(st, a, reinterpret_cast<hipStream_t>(stream), &kp.ap);
-        if (rc != MK_OK) return rc;
+        kp.attn_params = a;
     }
     kp.pos = g->pos_id;
     // fn is one of the four instantiations above

@@ -219,3 +219,32 @@ def to_device(model, device):
         model=SimpleNamespace(rope_cos=mv(model.model.rope_cos), rope_sin=mv(model.model.rope_sin)),
         generator=None,
     )
+
+
+def slice_layers(model, layers: int, device="cpu"):
+    """The first ``layers`` layers of a synthetic model (stacked weights and
+    KV cache), with its embeddings, LM head and RoPE tables, copied to
+    ``device``: a whole-model schedule over the slice runs the same
+    per-layer work at the same shapes."""
+    device = torch.device(device)
+
+    def mv(t, cut=True):
+        if t is None:
+            return None
+        t = t[:layers] if cut and t.dim() > 0 and t.shape[0] == model.config.num_hidden_layers else t
+        return t.to(device).contiguous()
+
+    sp = model.stacked_params
+    params = StackedMoEParams(**{k: mv(v) for k, v in vars(sp).items()})
+    return SimpleNamespace(
+        config=with_layers(model.config, layers),
+        device=device,
+        dtype=model.dtype,
+        stacked_params=params,
+        lm_head=SimpleNamespace(input_norm=SimpleNamespace(weight=mv(model.lm_head.input_norm.weight, False)),
+                                lm_head=SimpleNamespace(weight=mv(model.lm_head.lm_head.weight, False))),
+        embed_tokens=mv(getattr(model, "embed_tokens", None), False),
+        stacked_kv_cache=tuple(mv(t) for t in model.stacked_kv_cache),
+        model=SimpleNamespace(rope_cos=mv(model.model.rope_cos, False), rope_sin=mv(model.model.rope_sin, False)),
+        generator=None,
+    )

@@ -16,6 +16,14 @@
  *     where noted.  The caller owns all memory; the kernel only borrows it.
  *   - Launches are asynchronous on `stream` (a `hipStream_t`, NULL = default
  *     stream).  Entry points never throw; they return an `mk_status_code`.
+ *   - Launches on one device run one at a time, in the order they are made
+ *     (from any host thread, mk_llama_launch included): a persistent kernel
+ *     needs every workgroup resident at once, and the library's scratch and
+ *     status words are per device.  A launch on a stream other than the
+ *     previous launch's makes its stream wait (hipStreamWaitEvent) for all
+ *     work queued on that previous stream so far; if that stream has been
+ *     destroyed, the launch synchronises the device first.  Work on the
+ *     previous stream queued after the wait is not waited for.
  *   - The caller zeroes (or pre-fills) `barriers` before each launch, as the
  *     reference's callers do (megakernels/generators.py:115-116,132).
  *
@@ -228,8 +236,7 @@ typedef struct mk_mixtral_globals {
      * partition whose blocks interleave across workers (worker w: blocks
      * w, w + W, ...), which makes column chunks complete early.  Applies to
      * MoE-only launches (qkv_weights NULL) with 8 experts; ignored
-     * otherwise.  Launches on one device must not overlap (the counters are
-     * per device). */
+     * otherwise. */
     int32_t downproj_overlap;
 } mk_mixtral_globals;
 

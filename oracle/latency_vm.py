@@ -90,7 +90,7 @@ def solve_downproj(globs: Globals, ins: DownProjResidual):
     assert globs.barriers[layer, ins.prev_opcode() - 1, 0] == expected_upgate_barrier(globs)
     R = globs.matvec_reduction_size
     c0 = ins.reduction_block_idx * R
-    w = globs.down_proj_weights[layer][:, c0:c0 + R].contiguous()
+    w = globs.down_proj_weights[layer][:, c0:c0 + R]
     vec = globs.silu_out[c0:c0 + R].contiguous()
     bs = globs.down_proj_block_size
     for b in range(ins.start_block_idx, ins.end_block_idx):

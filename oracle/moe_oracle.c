@@ -134,10 +134,13 @@ void orc_down_accumulate(const uint16_t *down, const uint16_t *act, int64_t F, i
     }
 }
 
-/* Plain bf16 matvec rows (lat/python_vm.py:29-47): out[i] = bf16(M[row0+i] . v). */
-void orc_matvec(const uint16_t *mat, const uint16_t *vec, int64_t K, int64_t row0, int64_t nrows, uint16_t *out) {
+/* Plain bf16 matvec rows (lat/python_vm.py:29-47): out[i] = bf16(M[row0+i] . v)
+ * over K columns; rows are `ld` elements apart (ld > K for a column block of
+ * a wider matrix, as the LM head's 2048-column reduction blocks are). */
+void orc_matvec(const uint16_t *mat, int64_t ld, const uint16_t *vec, int64_t K, int64_t row0, int64_t nrows,
+                uint16_t *out) {
 #pragma omp parallel for schedule(static)
-    for (int64_t i = 0; i < nrows; ++i) out[i] = f2bf((float)dot_bf16(mat + (row0 + i) * K, vec, K));
+    for (int64_t i = 0; i < nrows; ++i) out[i] = f2bf((float)dot_bf16(mat + (row0 + i) * ld, vec, K));
 }
 
 /* Exported conversions so tests can pin the rounding helpers themselves. */

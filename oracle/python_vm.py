@@ -82,7 +82,7 @@ def lib():
         L.orc_router_logits.argtypes = [P, P, I64, I64, P, P]
         L.orc_upgate_silu.argtypes = [P, P, P, I64, I64, I64, P]
         L.orc_down_accumulate.argtypes = [P, P, I64, I64, I64, F32, P]
-        L.orc_matvec.argtypes = [P, P, I64, I64, I64, P]
+        L.orc_matvec.argtypes = [P, I64, P, I64, I64, I64, P]
         L.orc_set_num_threads.argtypes = [ctypes.c_int]
         L.orc_get_num_threads.restype = ctypes.c_int
         L.orc_f32_to_bf16.argtypes = [F32]
@@ -143,12 +143,16 @@ def router_logits(router_w: torch.Tensor, normed: torch.Tensor, bias: torch.Tens
 
 
 def matvec(mat: torch.Tensor, vec: torch.Tensor, row0: int = 0, nrows: int | None = None) -> torch.Tensor:
-    """bf16 rows ``mat[row0:row0+nrows] @ vec`` -- lat/python_vm.py:29-47."""
-    _cpu(mat, torch.bfloat16)
+    """bf16 rows ``mat[row0:row0+nrows] @ vec`` -- lat/python_vm.py:29-47.
+    ``mat`` may be a column block of a wider matrix (unit column stride)."""
+    if mat.device.type != "cpu" or mat.dtype != torch.bfloat16 or mat.dim() != 2 or mat.stride(1) != 1:
+        raise ValueError("matvec needs a CPU bf16 matrix with contiguous rows")
     _cpu(vec, torch.bfloat16)
     nrows = mat.shape[0] - row0 if nrows is None else nrows
+    if not 0 <= row0 <= row0 + nrows <= mat.shape[0] or vec.numel() != mat.shape[1]:
+        raise ValueError("matvec: rows or vector length out of range")
     out = torch.empty(nrows, dtype=torch.bfloat16)
-    lib().orc_matvec(_p(mat), _p(vec), mat.shape[1], row0, nrows, _p(out))
+    lib().orc_matvec(_p(mat), mat.stride(0), _p(vec), mat.shape[1], row0, nrows, _p(out))
     return out
 
 
@@ -406,7 +410,7 @@ def solve_lm_head(globs: MixtralGlobals, ins: Mixtral_RMS_LM_Head):
     post_ln = rms_norm(globs.hidden_states, globs.lm_head_norm_weights.reshape(-1).contiguous(), globs.rms_norm_eps)
     c0 = ins.reduction_block_idx * LM_HEAD_REDUCTION
     cols = slice(c0, c0 + LM_HEAD_REDUCTION)
-    w = globs.lm_head_weights[:, cols].contiguous()
+    w = globs.lm_head_weights[:, cols]
     vec = post_ln[cols].contiguous()
     bs = globs.lm_head_block_size
     for b in range(ins.start_output_block_idx, ins.end_output_block_idx):

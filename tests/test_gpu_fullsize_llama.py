@@ -1,0 +1,80 @@
+"""Full-size properties of Llama-3.2-3B-shaped decode on the dense VM
+28 layers, vocab 128256, the KV cache pre-filled to
+2048 positions.  The two-layer slice at the same shape is checked against
+the oracle in test_gpu_configs.py; here, what holds at any size:
+
+* the token the launch writes equals torch.argmax of the logits it left;
+* the barrier tensor equals its closed forms (lat/python_vm.py's arrivals):
+  per layer every QKV head counter at head_dim / qkv_block_size, every query
+  head's partial counter at the partition count, Hq reduced heads,
+  H / o_proj_block_size O-proj blocks, F / up_gate_proj_block_size up/gate
+  blocks and (F / matvec_reduction_size) (H / down_proj_block_size)
+  down-projection chunks, zero elsewhere;
+* a relaunch from the same input stays within max-abs-rel 2e-2 of the first
+  (the down projection adds its column chunks in arrival order, so the
+  dense VM is reproducible to bf16 rounding, not bit for bit).
+"""
+
+import pytest
+import torch
+
+from megakernels_amd.latency.synthetic import C3, make_synthetic_llama
+from megakernels_amd.mixtral.generate import MK_Generator
+from moe_harness import max_abs_rel
+
+pytestmark = pytest.mark.gpu
+
+PREFILL = 2048
+
+
+@pytest.fixture(scope="module")
+def model():
+    m = make_synthetic_llama(C3, "cuda", 51, kv_positions=PREFILL + 4, prefill=PREFILL)
+    torch.cuda.synchronize()
+    yield m
+    del m
+    torch.cuda.empty_cache()
+
+
+def _launch(gen, token: int, pos: int):
+    import mk_llama
+    from megakernels_amd.latency.mk import interpret_with_mk
+
+    g = gen.schedule.globs
+    g.hidden_states.copy_(gen.model.embed_tokens[token])
+    g.barriers.zero_()
+    g.logits.zero_()
+    g.pos_id = pos
+    out = torch.full((), -1, dtype=torch.long, device="cuda")
+    interpret_with_mk(g, mk_llama.mk_llama, argmax_out=out, debug_sync=True)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_fullsize_dense_decode_properties(model):
+    gen = MK_Generator.build(model, PREFILL)
+    g = gen.schedule.globs
+    linear = gen.schedule.get_linear_instructions()
+    nparts = max(i.num_partials for i in linear if i.opcode() == 2)
+    tok = _launch(gen, 777, PREFILL)
+    logits = g.logits.cpu()
+    assert bool(torch.isfinite(logits.float()).all()) and bool(logits.float().abs().max() > 0)
+    assert int(tok) == int(torch.argmax(logits)), "in-launch argmax differs from torch.argmax"
+
+    L, Hq, Hkv = g.num_hidden_layers, g.num_attention_heads, g.num_kv_heads
+    bar = torch.zeros_like(g.barriers, device="cpu")
+    bar[:, 0, :Hq + 2 * Hkv] = g.head_dim // g.qkv_block_size
+    if not g.skip_attn_reduction:
+        bar[:, 1, :Hq] = nparts
+    bar[:, 2, 0] = Hq
+    bar[:, 3, 0] = g.hidden_size // g.o_proj_block_size
+    bar[:, 4, 0] = g.intermediate_size // g.up_gate_proj_block_size
+    bar[:, 5, 0] = (g.intermediate_size // g.matvec_reduction_size) * (g.hidden_size // g.down_proj_block_size)
+    assert torch.equal(g.barriers.cpu(), bar), "barrier tensor differs from its closed forms"
+
+    hidden = g.hidden_states.cpu()
+    tok2 = _launch(gen, 777, PREFILL)
+    print(f"[fullsize c3] tokens {int(tok)} / {int(tok2)}, relaunch logits max-abs-rel "
+          f"{max_abs_rel(g.logits, logits):.1e}", flush=True)
+    assert max_abs_rel(g.logits, logits) <= 2e-2
+    assert max_abs_rel(g.hidden_states, hidden) <= 2e-2

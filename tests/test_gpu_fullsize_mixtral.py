@@ -1,0 +1,98 @@
+"""Full-size properties of Mixtral-8x7B-shaped decode (BASELINE configs 4
+and 5): all 32 layers, vocab 32000, 94 GB of weights resident, the KV cache
+pre-filled to 16384 positions.  The oracle cannot hold this model on the
+host, so these check what holds at any size (the two-layer slices at the
+same shapes are checked against the oracle in test_gpu_configs.py):
+
+* the token the launch writes (argmax inside the launch) equals
+  torch.argmax of the logits the same launch left, on the CPU;
+* the barrier tensor equals its closed forms (mkm/python_vm.py:38-54 and the
+  arrivals of each solver): per layer, every QKV head counter at
+  head_dim / qkv_block_size, every query head's partial counter at the
+  partition count, Hq reduced heads, H / o_proj_block_size O-proj blocks,
+  F / expert_proj_block_size up/gate blocks, 2 H / down_proj_block_size
+  down blocks and one prediction, and zero elsewhere;
+* a relaunch from the same input is bit-identical (token, logits, residual,
+  the appended K/V rows): the Mixtral path adds in a fixed order;
+* the logits are finite and not all zero.
+
+Config 4 decodes at position 4096 and config 5 at 16384 (predictor weights =
+router + N(0, 0.007)), from one model.
+"""
+
+import pytest
+import torch
+
+from megakernels_amd.mixtral.generate import MK_Generator
+from megakernels_amd.mixtral.synthetic import C4, make_synthetic_mixtral
+
+pytestmark = pytest.mark.gpu
+
+PREFILL_C5 = 16384
+
+
+@pytest.fixture(scope="module")
+def model():
+    m = make_synthetic_mixtral(C4, "cuda", 50, full=True, kv_positions=PREFILL_C5 + 4, prefill=PREFILL_C5,
+                               predictor_sigma=0.007)
+    torch.cuda.synchronize()
+    print(f"[fullsize] {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated", flush=True)
+    yield m
+    del m
+    torch.cuda.empty_cache()
+
+
+def _launch(gen, token: int, pos: int):
+    import mk_mixtral
+    from megakernels_amd.mixtral.mk import interpret_with_mk
+
+    g = gen.schedule.globs
+    g.hidden_states.copy_(gen.model.embed_tokens[token])
+    g.barriers.zero_()
+    g.logits.zero_()
+    g.pos_id = pos
+    out = torch.full((), -1, dtype=torch.long, device="cuda")
+    interpret_with_mk(g, mk_mixtral.mk_mixtral, argmax_out=out, debug_sync=True)
+    torch.cuda.synchronize()
+    return out
+
+
+def expected_barriers(g, nparts: int) -> torch.Tensor:
+    L, Hq, Hkv = g.num_hidden_layers, g.num_attention_heads, g.num_kv_heads
+    bar = torch.zeros_like(g.barriers, device="cpu")
+    bar[:, 0, :Hq + 2 * Hkv] = g.head_dim // g.qkv_block_size
+    if not g.skip_attn_reduction:
+        bar[:, 1, :Hq] = nparts
+    bar[:, 2, 0] = Hq
+    bar[:, 3, 0] = g.hidden_size // g.o_proj_block_size
+    bar[:, 4, 0] = g.intermediate_size // g.expert_proj_block_size
+    bar[:, 5, 0] = g.num_experts_per_tok * (g.hidden_size // g.down_proj_block_size)
+    bar[:, 7, 0] = 1
+    return bar
+
+
+@pytest.mark.parametrize("pos", [4096, PREFILL_C5], ids=["c4", "c5"])
+def test_fullsize_decode_properties(model, pos):
+    gen = MK_Generator.build(model, pos)
+    g = gen.schedule.globs
+    nparts = max(i.num_partials for i in gen.schedule.get_linear_instructions() if i.opcode() == 2)
+    print(f"[fullsize pos {pos}] {len(gen.schedule.dag_nodes)} instructions, {nparts} partitions", flush=True)
+    tok = _launch(gen, 1234, pos)
+    logits = g.logits.cpu()
+    assert bool(torch.isfinite(logits.float()).all()) and bool(logits.float().abs().max() > 0)
+    ref_tok = int(torch.argmax(logits))
+    assert int(tok) == ref_tok, f"in-launch argmax {int(tok)} != torch.argmax {ref_tok}"
+    assert torch.equal(g.barriers.cpu(), expected_barriers(g, nparts)), "barrier tensor differs from its closed forms"
+
+    first = {"logits": logits.clone(), "hidden": g.hidden_states.cpu(), "k": g.k_cache[:, 0, pos].cpu(),
+             "v": g.v_cache[:, 0, pos].cpu(), "sel": g.selected_expert_indices.cpu(),
+             "pred": g.predicted_expert_indices.cpu()}
+    tok2 = _launch(gen, 1234, pos)
+    assert int(tok2) == int(tok)
+    again = {"logits": g.logits.cpu(), "hidden": g.hidden_states.cpu(), "k": g.k_cache[:, 0, pos].cpu(),
+             "v": g.v_cache[:, 0, pos].cpu(), "sel": g.selected_expert_indices.cpu(),
+             "pred": g.predicted_expert_indices.cpu()}
+    for k in first:
+        assert torch.equal(first[k], again[k]), f"relaunch changed {k}"
+    print(f"[fullsize pos {pos}] token {int(tok)}, last layer experts {first['sel'].tolist()} "
+          f"(predicted {first['pred'].tolist()})", flush=True)

@@ -62,3 +62,33 @@ def test_timed_generate_runs_without_host_syncs():
     import mk_mixtral
 
     mk_mixtral.raise_if_failed("cuda")
+
+
+def test_two_generators_on_two_streams():
+    """Two decoders with their own weights, caches and barrier tensors,
+    stepped alternately on two streams with no host synchronisation between
+    the steps.  Launches on one device run one at a time (the library makes
+    a launch on a new stream wait for the previous launch's stream), so both
+    token streams equal the oracle's."""
+    prompt_len, ntok = 40, 4
+    cpus = [make_synthetic_mixtral(TINY, "cpu", seed, full=True, kv_positions=prompt_len + ntok + 1,
+                                   prefill=prompt_len, ln_weight_std=0.1) for seed in (31, 32)]
+    gens = [MK_Generator.build(to_device(c, "cuda"), prompt_len) for c in cpus]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    toks = [torch.zeros(1, ntok + 1, dtype=torch.long, device="cuda") for _ in gens]
+    for t, first in zip(toks, (7, 9)):
+        t[0, 0] = first
+    torch.cuda.synchronize()
+    for i in range(ntok):
+        for gen, st, t in zip(gens, streams, toks):
+            with torch.cuda.stream(st):
+                gen.generate(t, prompt_len, 1, ntok_already_generated=i + 1)
+    torch.cuda.synchronize()
+    import mk_mixtral
+
+    mk_mixtral.raise_if_failed("cuda")
+    W = gens[0].schedule.globs.sm_count()
+    for cpu, t, first in zip(cpus, toks, (7, 9)):
+        ref, _ = _oracle_generate(cpu, prompt_len, first, ntok, W)
+        print(f"[two streams] gpu {t[0].tolist()} oracle {ref}", flush=True)
+        assert t[0].tolist() == ref

@@ -286,3 +286,22 @@ def test_predictor_uses_predictor_weights():
     normed = oracle.rms_norm(g.hidden_states, sp.ffn_ln_weight[0], SMALL.rms_norm_eps)
     expect, _, _ = oracle.select_top_k(oracle.router_logits(sp.predictor_weight[0], normed), 2)
     assert g.predicted_expert_indices.tolist() == expect.tolist()
+
+
+def test_matvec_column_block_against_fp64():
+    """A 2048-column block of a wider matrix (the LM head's reduction blocks,
+    read in place through the row stride) equals the fp64 dot products
+    rounded once to bf16 (within one bf16 step, fp32 accumulation), and
+    equals the same block copied out first, bit for bit."""
+    g = torch.Generator().manual_seed(31)
+    w = (torch.randn(64, 6144, generator=g) * 0.02).to(torch.bfloat16)
+    v = torch.randn(2048, generator=g).to(torch.bfloat16)
+    blk = w[:, 2048:4096]
+    assert not blk.is_contiguous()
+    got = oracle.matvec(blk, v, 8, 40)
+    assert torch.equal(got, oracle.matvec(blk.contiguous(), v, 8, 40))
+    ref = (blk[8:48].double() @ v.double()).to(torch.bfloat16)
+    diff = (got.float() - ref.float()).abs()
+    assert float(diff.max()) <= float(ref.float().abs().max()) * 2 ** -7
+    # the wrong block (a transposed or shifted read) does not match
+    assert not torch.equal(got, oracle.matvec(w[:, :2048], v, 8, 40))
