@@ -2340,7 +2340,10 @@ __device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &s
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
-    if (threadIdx.x == 0) sh.stage_slot = -1;  // every thread has read it (the wait ends in barriers)
+    if (threadIdx.x == 0) {
+        sh.stage_slot = -1;  // every thread has read it (the wait ends in barriers)
+        sh.route_layer = layer;  // this layer's O projection is complete: its residual rows are final
+    }
     rms_to_lds(p, sh, act, p.ffn_ln + (size_t)layer * p.H);
     for (int it = wave; it < S; it += kWaves) {  // the staged items
         const int k = it / p.expert_bs;
@@ -2445,6 +2448,72 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
     return true;
 }
 
+// Opcode 6 when the column chunk is all of F (matvec_reduction_size == F):
+// every row has one writer, so h = bf16(h + bf16(W[r] . silu)) is a plain
+// coherent read-modify-write in python_vm's order, with no atomics, and a
+// relaunch is bit-identical.  Rows [start, end) * down_proj_block_size in
+// batches of kRowBatch; an item is one full row (nc chunks, up to kSegChunks
+// loads per lane in flight), its sum kept in LDS until the batch ends; the
+// first item of each wave is loaded before the wait, and, when this
+// workgroup's opcode 5 already passed the O-proj wait (the residual rows are
+// final then), so are the first batch's residual rows.
+__device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+                                                int32_t *tim, int layer, int b0, int b1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = b0 * p.down_bs, nrows = (b1 - b0) * p.down_bs;
+    const int nc = p.F / kChunkElems;
+    const uint16_t *wm = p.down + (size_t)layer * p.H * p.F;
+    const int first_batch = min(nrows, kRowBatch);
+    RowRegs<kEarlyChunks> pre;
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    if (wave < first_batch)
+        load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + wave) * p.F) + lane,
+                               min(nc, kEarlyChunks));
+    const bool hfinal = __builtin_amdgcn_readfirstlane(sh.route_layer) == layer;
+    uint32_t hpre = 0;
+    if (hfinal && tid < first_batch) hpre = ld_dev16(p.hidden + r0 + tid);
+    stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
+    if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
+    stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    for (int v = tid; v < (p.F >> 3); v += kThreads) act[v] = ld_dev128(p.silu, (uint32_t)v * 16u);
+    __syncthreads();
+    float *part = sh.part;  // one fp32 sum per row of the batch
+    for (int bb = 0; bb < nrows; bb += kRowBatch) {
+        const int nb_rows = min(kRowBatch, nrows - bb);
+        for (int it = wave; it < nb_rows; it = next_local_item(sh, lane)) {
+            const u32x4 *w = reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + bb + it) * p.F) + lane;
+            const u32x4 *x = act + lane;
+            float acc = 0.f;
+            int done = 0;
+            if (bb == 0 && it == wave) {
+                done = min(nc, kEarlyChunks);
+                acc = dot_row_regs<kEarlyChunks>(pre, x, done, acc);
+            }
+            while (done < nc) {
+                const int n = min(nc - done, kSegChunks);
+                RowRegs<kSegChunks> r;
+                load_row<kSegChunks>(r, w + done * 64, n);
+                acc = dot_row_regs<kSegChunks>(r, x + done * 64, n, acc);
+                done += n;
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) part[it] = acc;
+        }
+        __syncthreads();
+        for (int r = tid; r < nb_rows; r += kThreads) {
+            uint16_t *hp = p.hidden + r0 + bb + r;
+            const uint32_t h = hfinal && bb == 0 ? hpre : ld_dev16(hp);  // r == tid in the first batch
+            st_dev16(hp, f2bf(bf2f(h) + rbf(part[r])));
+        }
+        if (tid == 0) sh.next_item = kWaves;
+        __syncthreads();
+    }
+    drain_and_sync();
+    arrive(bar_at(p, layer, 6), b1 - b0);
+    stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
+    return true;
+}
+
 __device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                               const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
@@ -2457,6 +2526,7 @@ __device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh,
         return false;
     }
     if (threadIdx.x == 0) sh.next_item = kWaves;
+    if (p.red_cols == p.F) return dense_down_full(p, sh, act, c, tim, layer, b0, b1);
     // the host admits red_cols of 1, 2, 4 or 8 chunks and even block sizes
     // that the row group divides
     switch (p.red_cols / kChunkElems) {
@@ -3041,10 +3111,11 @@ int validate_llama(const mk_llama_globals *g) {
     if (g->bar_width < Hq + 2 * Hkv) return MK_ERR_INVALID_ARGUMENT;
     const int R = g->matvec_reduction_size;
     if (R < kChunkElems || R % kChunkElems || F % R) return MK_ERR_UNSUPPORTED;
-    // opcode 6 takes items of 16 / (R / 512) rows x R / 512 chunks
+    // opcode 6 takes full rows when R == F, else items of 16 / (R / 512)
+    // rows x R / 512 chunks
     const int rc = R / kChunkElems;
-    if (rc != 1 && rc != 2 && rc != 4 && rc != 8) return MK_ERR_UNSUPPORTED;
-    if (g->down_proj_block_size % (16 / rc)) return MK_ERR_UNSUPPORTED;
+    if (R != F && rc != 1 && rc != 2 && rc != 4 && rc != 8) return MK_ERR_UNSUPPORTED;
+    if (R != F && g->down_proj_block_size % (16 / rc)) return MK_ERR_UNSUPPORTED;
     if (g->up_gate_proj_block_size < 1 || F % g->up_gate_proj_block_size || g->down_proj_block_size < 2 ||
         g->down_proj_block_size % 2 || H % g->down_proj_block_size || g->o_proj_block_size < 2 ||
         g->o_proj_block_size % 2 || H % g->o_proj_block_size)

@@ -5,8 +5,11 @@ Counterpart of ``megakernels/demos/latency/scheduler.py:1-440``:
 * ``make_globals`` allocates the reference's buffers with the same shapes and
   dtypes (``:39-147``): barriers ``[L, 10, Hq + 2*Hkv]`` int32, ``silu_out
   [F]``, attention intermediates sized by the worker count, block sizes 16;
-  ``matvec_reduction_size`` is F / 4 where the kernel takes that width
-  (``default_reduction_size``; the reference's gcd(F, H) otherwise).
+  ``matvec_reduction_size`` is the whole FFN width F (one column chunk:
+  every residual row has one writer, so the down projection adds in
+  python_vm's order and relaunches are bit-identical;
+  ``default_reduction_size``), with down-projection blocks sized to spread
+  the rows evenly (``default_down_block_size``).
 * the partitioners follow ``:150-264``: QKV and LM-head blocks in contiguous
   banker's-rounded spans, up/gate blocks strided by the worker count, and
   down-projection (column chunk, row block) jobs split over workers so that
@@ -34,7 +37,7 @@ import torch
 from ..instructions import NoOp
 from ..scheduler import DAG_Node, ScheduleBuilder
 from ..utils import assert_div, get_sm_count
-from ..mixtral.scheduler import pick_num_attention_partitions
+from ..mixtral.scheduler import pick_block_size, pick_num_attention_partitions
 from .instructions import (
     AttentionReduction,
     DownProjResidual,
@@ -52,16 +55,25 @@ BARRIER_OPS = 10
 
 def default_reduction_size(intermediate: int, hidden: int) -> int:
     """Column chunk of the dense down-projection (``matvec_reduction_size``):
-    a quarter of the FFN width when that is 512, 1024, 2048 or 4096 columns,
-    else gcd(F, H) as before.  Four chunks per row measured best at the 3B
-    shape (F = 8192: 2048 -> 547.3 tokens/s, 1024 -> 528.2, 4096 -> 540.5,
-    512 -> 489.8): each chunk of a row is a separate job whose partial is
-    added into the residual with a packed bf16 atomic, so fewer chunks mean
-    fewer jobs and atomics, and more mean more parallelism."""
-    r = intermediate // 4
-    if intermediate % 4 == 0 and r in (512, 1024, 2048, 4096):
-        return r
+    the whole FFN width when it is a multiple of 512.  Each row then has a
+    single writer, which adds its one bf16 partial into the residual with a
+    plain read-modify-write in python_vm's order, so results are
+    reproducible bit for bit.  With narrower chunks the partials of a row
+    come from different workers and are added with packed bf16 atomics in
+    arrival order (python_vm adds them in chunk order), which made relaunches
+    of the 28-layer 3B shape drift by 4 % in the logits."""
+    if intermediate % 512 == 0:
+        return intermediate
     return math.gcd(intermediate, hidden)
+
+
+def default_down_block_size(hidden: int, workers: int, reduction: int, intermediate: int) -> int:
+    """Rows per down-projection block: with full-width rows, the size that
+    leaves the busiest worker the fewest rows (3B shape, 256 workers: 4 rows,
+    768 blocks, 12 rows per worker); with column chunks, the reference's 16."""
+    if reduction == intermediate:
+        return pick_block_size(hidden, workers, (16, 8, 4, 2))
+    return 16
 
 
 def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 0,
@@ -90,6 +102,8 @@ def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 
         skip_attn_reduction = parts == 1
     sp = model.stacked_params
     Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    reduction = block_sizes.get("matvec_reduction_size",
+                                default_reduction_size(cfg.intermediate_size, cfg.hidden_size))
 
     def buf(shape, buf_dtype=dtype):
         return torch.zeros(shape, device=device, dtype=buf_dtype)
@@ -129,11 +143,11 @@ def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 
         logits=buf(cfg.vocab_size),
         skip_attn_reduction=skip_attn_reduction,
         up_gate_proj_block_size=block_sizes.get("up_gate_proj_block_size", 16),
-        down_proj_block_size=block_sizes.get("down_proj_block_size", 16),
+        down_proj_block_size=block_sizes.get("down_proj_block_size", default_down_block_size(
+            cfg.hidden_size, workers, reduction, cfg.intermediate_size)),
         o_proj_block_size=block_sizes.get("o_proj_block_size", 16),
         lm_head_block_size=block_sizes.get("lm_head_block_size", 16),
-        matvec_reduction_size=block_sizes.get("matvec_reduction_size",
-                                              default_reduction_size(cfg.intermediate_size, cfg.hidden_size)),
+        matvec_reduction_size=reduction,
         # 16-row QKV blocks: the kernel stages a block's rows on chip before
         # its wait, so fewer, larger blocks pay (config 3: 547.3 -> 550.4
         # tokens/s against 8-row blocks)

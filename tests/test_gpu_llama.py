@@ -41,15 +41,19 @@ def test_upgate_stage():
     _check(case, "upgate")
 
 
-@pytest.mark.parametrize("config,prefill", [(LLAMA_SMALL, 20), (LLAMA_SMALL, 400), (LLAMA_TINY, 300)])
-def test_full_model_steps(config, prefill):
+@pytest.mark.parametrize("config,prefill,red", [(LLAMA_SMALL, 20, None), (LLAMA_SMALL, 400, None),
+                                                (LLAMA_TINY, 300, None), (LLAMA_SMALL, 400, 512),
+                                                (LLAMA_TINY, 300, 512)])
+def test_full_model_steps(config, prefill, red):
     """Two layers and the LM head, three consecutive steps: the down
-    projection's column chunks (packed bf16 atomics into the residual) and
-    the stored logits."""
-    case = LlamaCase(config, seed=4, prefill=prefill, steps=3, workers=64)
+    projection over full rows (the default, one writer per residual row) or
+    in 512-column chunks (packed bf16 atomics into the residual), and the
+    stored logits."""
+    kw = {} if red is None else {"matvec_reduction_size": red}
+    case = LlamaCase(config, seed=4, prefill=prefill, steps=3, workers=64, **kw)
     for tok in (5, 17, 200):
         case.step(tok)
-        _check(case, f"llama {config.hidden_size} prefill {prefill}")
+        _check(case, f"llama {config.hidden_size} prefill {prefill} R {case.g_gpu.matvec_reduction_size}")
         g, r = case.g_gpu.logits.float().cpu(), case.g_cpu.logits.float()
         top_g, top_r = int(g.argmax()), int(r.argmax())
         assert top_g == top_r or float(r[top_r] - r[top_g]) <= 2 ** -6 * float(r.abs().max())

@@ -88,6 +88,24 @@ def test_downproj_jobs_cover_each_chunk_once(workers):
     assert len(down) <= max(workers, 4)  # at least one instruction per column chunk
 
 
+def test_full_row_down_projection_defaults_at_3b():
+    """The 3B shape at 256 workers: one column chunk of 8192 and 4-row
+    blocks, i.e. 768 single-chunk jobs, three (12 rows, 192 KiB) per worker."""
+    from megakernels_amd.latency.scheduler import default_down_block_size, default_reduction_size
+
+    R = default_reduction_size(8192, 3072)
+    bs = default_down_block_size(3072, 256, R, 8192)
+    assert (R, bs) == (8192, 4)
+    g = _G(C3, 256)
+    g.matvec_reduction_size, g.down_proj_block_size = R, bs
+    down = schedule_downproj(g, 0)
+    assert len(down) == 256 and all(i.reduction_block_idx == 0 for i in down)
+    assert sorted(b for i in down for b in range(i.start_block_idx, i.end_block_idx)) == list(range(768))
+    assert {i.end_block_idx - i.start_block_idx for i in down} == {3}
+    # narrower chunks keep the reference's 16-row blocks
+    assert default_down_block_size(3072, 256, 2048, 8192) == 16
+
+
 def test_make_globals_buffers():
     model = make_synthetic_llama(LLAMA_SMALL, "cpu", 0, kv_positions=64, prefill=20)
     g = make_globals(model, seq_len=20, sm_count=16)
@@ -95,7 +113,9 @@ def test_make_globals_buffers():
     assert g.barriers.shape == (2, 10, Hq + 2 * Hkv) and g.barriers.dtype == torch.int32
     assert g.silu_out.shape == (F,) and g.logits.shape == (512,)
     assert g.attn_lse_intermediates.shape == (Hq, 16) and g.attn_out_intermediates.shape == (Hq, 16, D)
-    assert g.matvec_reduction_size == 512 and g.attn_reduction_size == 3
+    # one column chunk (full rows, single writer per residual row)
+    assert g.matvec_reduction_size == F and g.attn_reduction_size == 3
+    assert g.down_proj_block_size == 16  # 96 rows on each of 16 workers at any of 16, 8, 4, 2
     assert g.attn_scale == pytest.approx(1 / math.sqrt(D))
     assert g.skip_attn_reduction  # 21 positions: one partition
 
@@ -116,7 +136,7 @@ def test_dag_structure(policy, parts):
     assert all(len(n.dependencies) == per_layer[4] for n in up0)
     down0 = [n for n in nodes if n.instruction.opcode() == 6 and n.instruction.layer_idx == 0]
     assert all(set(map(id, n.dependencies)) == set(map(id, up0)) for n in down0)
-    assert expected_downproj_arrivals(g) == 4 * (1536 // 16)
+    assert expected_downproj_arrivals(g) == (2048 // g.matvec_reduction_size) * (1536 // g.down_proj_block_size)
 
 
 @pytest.mark.parametrize("seq,kv,W", [(1, 8, 256), (64, 8, 256), (65, 8, 256), (2049, 8, 256), (4097, 8, 256),

@@ -18,10 +18,10 @@ from oracle import python_vm as mx
 BF16 = torch.bfloat16
 
 
-def _globals(cfg, layers=None, seed=3, prefill=40, workers=16):
+def _globals(cfg, layers=None, seed=3, prefill=40, workers=16, **block_sizes):
     cfg = with_layers(cfg, layers) if layers else cfg
     model = make_synthetic_llama(cfg, "cpu", seed, ln_weight_std=0.1, kv_positions=prefill + 4, prefill=prefill)
-    g = make_globals(model, seq_len=prefill, sm_count=workers)
+    g = make_globals(model, seq_len=prefill, sm_count=workers, **block_sizes)
     g.pos_id = prefill
     return model, g
 
@@ -58,7 +58,7 @@ def test_upgate_against_fp64_and_its_rounding():
 
 
 def test_downproj_column_chunks_add_up_to_the_full_matvec():
-    model, g = _globals(LLAMA_SMALL, layers=1)
+    model, g = _globals(LLAMA_SMALL, layers=1, matvec_reduction_size=512)
     gen = torch.Generator().manual_seed(2)
     g.silu_out.copy_(torch.randn(g.intermediate_size, generator=gen).to(BF16))
     h0 = torch.randn(g.hidden_size, generator=gen).to(BF16)
@@ -165,7 +165,7 @@ def test_oproj_uses_every_attention_column():
     past that prefix must change the result."""
     from megakernels_amd.latency.instructions import O_ProjResidual
 
-    model, g = _globals(LLAMA_SMALL, layers=1)
+    model, g = _globals(LLAMA_SMALL, layers=1, matvec_reduction_size=512)
     assert g.matvec_reduction_size < g.num_attention_heads * g.head_dim
     gen = torch.Generator().manual_seed(5)
     g.attn_out.copy_(torch.randn(g.attn_out.shape, generator=gen).to(BF16))

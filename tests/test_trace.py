@@ -114,19 +114,21 @@ def test_record_roundtrip_keeps_attention_fields(tmp_path):
     assert (back.head_dim, back.num_kv_heads, back.attn_kv_block_size, back.pos_id) == (128, 8, 16, 4096)
 
 
-def test_dense_vm_byte_model_covers_each_weight_once():
+@pytest.mark.parametrize("red", [512, 2048])
+def test_dense_vm_byte_model_covers_each_weight_once(red):
     """For the dense (Llama) VM the per-instruction byte model adds up to
-    each layer's up+gate, down and O/QKV weights, and the LM head, once."""
+    each layer's up+gate, down and O/QKV weights, and the LM head, once
+    (down projection in column chunks of 512, or full rows)."""
     from megakernels_amd.latency.scheduler import make_dag, make_globals
     from megakernels_amd.latency.synthetic import LLAMA_SMALL, make_synthetic_llama
     from megakernels_amd.scheduler import Schedule, assign_to_sms, tensorize_instructions
 
     model = make_synthetic_llama(LLAMA_SMALL, "cpu", 0, kv_positions=64, prefill=40)
-    g = make_globals(model, seq_len=40, sm_count=16)
+    g = make_globals(model, seq_len=40, sm_count=16, matvec_reduction_size=red)
     g.pos_id = 40
     tensorize_instructions(g, assign_to_sms("rr", schedule=Schedule(g, *make_dag(g))))
     rec = TimingRecord.from_globals(g)
-    assert rec.dense and rec.red_cols == 512 and rec.opcode_names[6] == "DownProjResidual"
+    assert rec.dense and rec.red_cols == red and rec.opcode_names[6] == "DownProjResidual"
     W, Q = rec.instructions.shape[:2]
     by_op = {}
     for w in range(W):
