@@ -2454,7 +2454,8 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
 // relaunch is bit-identical.  Rows [start, end) * down_proj_block_size in
 // batches of kRowBatch; an item is one full row (nc chunks, up to kSegChunks
 // loads per lane in flight), its sum kept in LDS until the batch ends; the
-// first item of each wave is loaded before the wait, and, when this
+// first item of each wave (its first kSegChunks chunks) is loaded before the
+// wait, and, when this
 // workgroup's opcode 5 already passed the O-proj wait (the residual rows are
 // final then), so are the first batch's residual rows.
 __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
@@ -2464,11 +2465,11 @@ __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &s
     const int nc = p.F / kChunkElems;
     const uint16_t *wm = p.down + (size_t)layer * p.H * p.F;
     const int first_batch = min(nrows, kRowBatch);
-    RowRegs<kEarlyChunks> pre;
+    RowRegs<kSegChunks> pre;  // up to a whole first row per wave (16 KiB), as many loads as a later item
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     if (wave < first_batch)
-        load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + wave) * p.F) + lane,
-                               min(nc, kEarlyChunks));
+        load_row<kSegChunks>(pre, reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + wave) * p.F) + lane,
+                             min(nc, kSegChunks));
     const bool hfinal = __builtin_amdgcn_readfirstlane(sh.route_layer) == layer;
     uint32_t hpre = 0;
     if (hfinal && tid < first_batch) hpre = ld_dev16(p.hidden + r0 + tid);
@@ -2478,25 +2479,29 @@ __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &s
     for (int v = tid; v < (p.F >> 3); v += kThreads) act[v] = ld_dev128(p.silu, (uint32_t)v * 16u);
     __syncthreads();
     float *part = sh.part;  // one fp32 sum per row of the batch
+    // the rest of row r0 + bb + it from chunk `done` on, added to acc
+    auto row_rest = [&](int bb, int it, int done, float acc) {
+        const u32x4 *w = reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + bb + it) * p.F) + lane;
+        while (done < nc) {
+            const int n = min(nc - done, kSegChunks);
+            RowRegs<kSegChunks> r;
+            load_row<kSegChunks>(r, w + done * 64, n);
+            acc = dot_row_regs<kSegChunks>(r, act + lane + done * 64, n, acc);
+            done += n;
+        }
+        return acc;
+    };
+    // the items loaded before the wait (outside the item loop, so their
+    // registers are free again for the later items)
+    if (wave < first_batch) {
+        const int n = min(nc, kSegChunks);
+        const float acc = wave_sum(row_rest(0, wave, n, dot_row_regs<kSegChunks>(pre, act + lane, n, 0.f)));
+        if (lane == 0) part[wave] = acc;
+    }
     for (int bb = 0; bb < nrows; bb += kRowBatch) {
         const int nb_rows = min(kRowBatch, nrows - bb);
-        for (int it = wave; it < nb_rows; it = next_local_item(sh, lane)) {
-            const u32x4 *w = reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + bb + it) * p.F) + lane;
-            const u32x4 *x = act + lane;
-            float acc = 0.f;
-            int done = 0;
-            if (bb == 0 && it == wave) {
-                done = min(nc, kEarlyChunks);
-                acc = dot_row_regs<kEarlyChunks>(pre, x, done, acc);
-            }
-            while (done < nc) {
-                const int n = min(nc - done, kSegChunks);
-                RowRegs<kSegChunks> r;
-                load_row<kSegChunks>(r, w + done * 64, n);
-                acc = dot_row_regs<kSegChunks>(r, x + done * 64, n, acc);
-                done += n;
-            }
-            acc = wave_sum(acc);
+        for (int it = bb == 0 ? next_local_item(sh, lane) : wave; it < nb_rows; it = next_local_item(sh, lane)) {
+            const float acc = wave_sum(row_rest(bb, it, 0, 0.f));
             if (lane == 0) part[it] = acc;
         }
         __syncthreads();

@@ -11,8 +11,9 @@ one position: the GPU kernel appends K/V at pos_id, as does the oracle.
 to and including that stage of layer 0 runs on the oracle, the state it
 leaves (activations, intermediates, K/V rows, barriers) is copied to the GPU,
 and the rest of the schedule runs on the kernel and on the oracle from that
-same state.  The stage under test then sees bit-identical inputs, so its
-rounding points are checked on their own, with no drift from earlier stages.
+same state.  With ``stop_after_op`` as well, the rest is just the stages
+between the two, so one stage can be run alone from bit-identical inputs and
+its rounding points checked with no drift from earlier stages.
 
 Large shapes (``generate_on_device=True``) draw the weights on the GPU and
 copy them to the host for the oracle: the same tensors on both sides, drawn
@@ -35,12 +36,14 @@ MUTABLE = ("hidden_states", "post_ln_rope_q", "attn_out", "attn_out_intermediate
            "selected_expert_scores", "predicted_expert_indices", "barriers", "k_cache", "v_cache")
 
 
-def split_linear(dag_fn, globs, start_after_op: str, layer_limit: int | None, **dag_kw):
+def split_linear(dag_fn, globs, start_after_op: str, layer_limit: int | None, stop_after_op: str | None = None,
+                 **dag_kw):
     """(prefix, suffix) of the linear instruction list of ``dag_fn(globs,
-    layer_limit=layer_limit)``: the prefix is the schedule that stops after
-    ``start_after_op`` in layer 0, which must be a prefix of the whole
-    (megakernels/scripts/diff_test.py:139-153)."""
-    nodes, end = dag_fn(globs, layer_limit=layer_limit, **dag_kw)
+    stop_after_op=stop_after_op, layer_limit=layer_limit)``: the prefix is
+    the schedule that stops after ``start_after_op`` in layer 0, which must
+    be a prefix of the whole (megakernels/scripts/diff_test.py:139-153).
+    With both, the suffix is the stages between the two."""
+    nodes, end = dag_fn(globs, stop_after_op=stop_after_op, layer_limit=layer_limit, **dag_kw)
     full = Schedule(globs, nodes, end).get_linear_instructions()
     pnodes, pend = dag_fn(globs, stop_after_op=start_after_op, layer_limit=1, **dag_kw)
     prefix = Schedule(globs, pnodes, pend).get_linear_instructions()
@@ -81,8 +84,8 @@ class FullCase:
             self.linear = self.schedule.get_linear_instructions()
             queues = assign_to_sms(mode, schedule=self.schedule)
         else:
-            assert stop_after_op is None
-            self.prefix, self.linear = split_linear(make_dag, self.g_gpu, start_after_op, layer_limit, **dag_kw)
+            self.prefix, self.linear = split_linear(make_dag, self.g_gpu, start_after_op, layer_limit, stop_after_op,
+                                                    **dag_kw)
             assert mode in ("rr", "zz"), "a schedule suffix is assigned from its instruction list"
             queues = assign_to_sms(mode, instructions=self.linear, sm_count=workers)
         self.g_cpu.skip_attn_reduction = self.g_gpu.skip_attn_reduction

@@ -45,8 +45,7 @@ class LlamaCase:
             self.linear = self.schedule.get_linear_instructions()
             queues = assign_to_sms(mode, schedule=self.schedule)
         else:
-            assert stop_after_op is None
-            self.prefix, self.linear = split_linear(make_dag, self.g_gpu, start_after_op, layer_limit)
+            self.prefix, self.linear = split_linear(make_dag, self.g_gpu, start_after_op, layer_limit, stop_after_op)
             assert mode in ("rr", "zz"), "a schedule suffix is assigned from its instruction list"
             queues = assign_to_sms(mode, instructions=self.linear, sm_count=workers)
         self.g_cpu.skip_attn_reduction = self.g_gpu.skip_attn_reduction

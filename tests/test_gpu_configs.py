@@ -60,6 +60,37 @@ def _check_through(tag, case):
     assert case.barriers_equal(), f"{tag}: barrier tensor differs from the oracle's"
 
 
+#: router-logit gap below which the last layer's selection may legitimately
+#: differ from the oracle's after whole-model steps (the residual differs by
+#: up to max-abs-rel ~1e-2 there); the layer-only tests draw inputs with a
+#: 1e-3 margin instead
+TIE_MARGIN = 0.05
+
+
+def _check_selection(case):
+    """The last layer's expert pair equal to the oracle's, in order, unless
+    the oracle's top-2 router logits are within TIE_MARGIN (then as a set)
+    or its 2nd and 3rd are (then the first expert only).  The predicted pair
+    is printed: the pre-attention residual it came from is not kept, so its
+    margins are unknown."""
+    from oracle import python_vm as oracle
+
+    g, r = case.g_gpu, case.g_cpu
+    last = g.num_hidden_layers - 1
+    gi, ri = case.indices()
+    logits = oracle.router_logits(r.router_weights[last].contiguous(), r.router_normed_hidden)
+    top = torch.sort(logits, descending=True).values
+    gap01, gap12 = float(top[0] - top[1]), float(top[1] - top[2])
+    print(f"[selection] {gi} oracle {ri} gaps {gap01:.3f} {gap12:.3f}; predicted "
+          f"{g.predicted_expert_indices.cpu().tolist()} oracle {r.predicted_expert_indices.tolist()}", flush=True)
+    if gap12 < TIE_MARGIN:
+        assert gi[0] == ri[0] or gap01 < TIE_MARGIN
+    elif gap01 < TIE_MARGIN:
+        assert sorted(gi) == sorted(ri)
+    else:
+        assert gi == ri, f"experts {gi} != oracle {ri}"
+
+
 def _check_stage(tag, case, exact_keys, one_ulp=()):
     """Every output within max-abs-rel; ``exact_keys`` at least 99 %
     bit-identical; ``one_ulp`` within one bf16 ulp everywhere."""
@@ -88,9 +119,7 @@ def test_mixtral_two_layers_at_config_shape(prefill, sigma):
     for tok in (11, 23000, 31999):
         case.step(tok)
         _check_through(f"{'c5' if sigma else 'c4'} x2", case)
-        gi, ri = case.indices()
-        assert gi == ri, f"expert indices {gi} != oracle {ri}"
-        assert case.g_gpu.predicted_expert_indices.cpu().tolist() == case.g_cpu.predicted_expert_indices.tolist()
+        _check_selection(case)
 
 
 # ---------------------------------------------------------------------------
@@ -108,54 +137,61 @@ def test_llama_two_layers_at_config_shape():
 # stages from the oracle's state, at the config-4 (and config-3) shapes
 # ---------------------------------------------------------------------------
 
-#: stage -> (outputs held to 99 % bit-identical, those also held to one ulp)
+#: one stage at a time, from the oracle's state: (after, through) -> (outputs
+#: held to 99 % bit-identical, those also held to one ulp); None: from the
+#: start of the step, or through the LM head
 MIXTRAL_STAGES = {
-    "qkv": (("k_new", "v_new", "q", "attn_out", "hidden", "normed", "silu"), ()),
-    "partial": (("attn_out", "hidden", "normed", "silu"), ()),
-    "reduction": (("attn_out", "hidden", "normed", "silu"), ()),
-    "oproj": (("hidden", "normed", "silu"), ("normed",)),
-    "rms_router_upgate": (("hidden",), ()),
-    "downproj": (("logits",), ()),
+    (None, "qkv"): (("k_new", "v_new", "q"), ()),
+    ("qkv", "reduction"): (("attn_out",), ()),          # partial attention + LSE reduction
+    ("partial", "reduction"): (("attn_out",), ()),      # LSE reduction alone
+    ("reduction", "oproj"): (("hidden",), ()),
+    ("oproj", "rms_router_upgate"): (("normed", "silu"), ("normed",)),
+    ("rms_router_upgate", "downproj"): (("hidden",), ()),  # opcode 6, routing read from memory
+    ("downproj", None): (("logits",), ()),               # the LM head
 }
 
 
-@pytest.mark.parametrize("start", list(MIXTRAL_STAGES))
-def test_mixtral_stages_from_oracle_state(start):
-    """One C4-shaped layer with the LM head, 4096 cached positions: the
-    prefix through ``start`` of layer 0 on the oracle, the rest on the kernel
-    and on the oracle from the same state.  ``rms_router_upgate``: opcode 6
-    reads the routing from memory (its workgroups did not route the layer);
-    ``downproj``: the LM head alone, from the oracle's final residual."""
+def _stage_id(stage):
+    return f"{stage[0] or 'start'}-{stage[1] or 'lm_head'}"
+
+
+@pytest.mark.parametrize("stage", list(MIXTRAL_STAGES), ids=_stage_id)
+def test_mixtral_stage_from_oracle_state(stage):
+    """One stage of a C4-shaped layer (4096 cached positions, vocab 32000):
+    the schedule through ``after`` of layer 0 on the oracle, then the stages
+    through ``through`` on the kernel and on the oracle from the same state."""
+    after, through = stage
     case = FullCase(with_layers(C4, 1), seed=42, prefill=4096, steps=2, generate_on_device=True,
-                    ln_weight_std=0.1, start_after_op=start)
+                    ln_weight_std=0.1, start_after_op=after, stop_after_op=through)
     for tok in (3, 17):
         case.step(tok)
-        keys, one_ulp = MIXTRAL_STAGES[start]
-        _check_stage(f"c4 from {start}", case, keys, one_ulp)
-        if start not in ("rms_router_upgate", "downproj"):
+        keys, one_ulp = MIXTRAL_STAGES[stage]
+        _check_stage(f"c4 {_stage_id(stage)}", case, keys, one_ulp)
+        if through == "rms_router_upgate":
             gi, ri = case.indices()
             assert gi == ri
 
 
 LLAMA_STAGES = {
-    "qkv": ("k_new", "v_new", "q", "attn_out", "hidden", "silu"),
-    "reduction": ("attn_out", "hidden", "silu"),
-    "oproj": ("hidden", "silu"),
-    "upgate": ("hidden",),
-    "downproj": ("logits",),
+    (None, "qkv"): ("k_new", "v_new", "q"),
+    ("qkv", "reduction"): ("attn_out",),
+    ("reduction", "oproj"): ("hidden",),
+    ("oproj", "upgate"): ("silu",),
+    ("upgate", "downproj"): ("hidden",),  # full-row down projection, one writer per row
+    ("downproj", None): ("logits",),
 }
 
 
-@pytest.mark.parametrize("start", list(LLAMA_STAGES))
-def test_llama_stages_from_oracle_state(start):
-    """One C3-shaped layer with the 128256-row LM head, 2048 cached
-    positions, the dense VM's default full-row down projection (one writer
-    per residual row, python_vm's order)."""
+@pytest.mark.parametrize("stage", list(LLAMA_STAGES), ids=_stage_id)
+def test_llama_stage_from_oracle_state(stage):
+    """One stage of a C3-shaped layer (2048 cached positions, the
+    128256-row LM head) on the dense VM, from the oracle's state."""
+    after, through = stage
     case = LlamaCase(with_layers(C3, 1), seed=43, prefill=2048, steps=2, generate_on_device=True,
-                     start_after_op=start)
+                     start_after_op=after, stop_after_op=through)
     for tok in (9, 100000):
         case.step(tok)
-        _check_stage(f"c3 from {start}", case, LLAMA_STAGES[start])
+        _check_stage(f"c3 {_stage_id(stage)}", case, LLAMA_STAGES[stage])
 
 
 # ---------------------------------------------------------------------------

@@ -2,8 +2,8 @@
 
 The kernel is checked against the oracle with max-abs-rel <= 2e-2 *and* the
 rounding-point check of ``moe_harness.assert_bf16_close``: at most one bf16
-ulp on normed hidden (four on SiLU), and at least 99 % of normed hidden,
-SiLU and hidden bit-identical.  Here mistakes a kernel could make are planted in a
+ulp on normed hidden, and at least 99 % of normed hidden, SiLU and hidden
+bit-identical.  Here mistakes a kernel could make are planted in a
 copy of the oracle's arithmetic on the CPU (never on the GPU), and the check
 must reject each of them while the oracle itself passes:
 
@@ -22,7 +22,7 @@ import pytest
 import torch
 
 from megakernels_amd.mixtral.synthetic import C1, make_residuals, make_synthetic_mixtral
-from moe_harness import MAX_ULP_SILU, TOL, assert_bf16_close, bf16_agreement, max_abs_rel
+from moe_harness import TOL, assert_bf16_close, bf16_agreement, max_abs_rel
 from oracle import python_vm as oracle
 
 
@@ -86,7 +86,7 @@ def test_single_rounded_silu_fails(layer):
     bad = (torch.nn.functional.silu(g) * u).to(torch.bfloat16)
     assert max_abs_rel(bad, ref) <= TOL
     with pytest.raises(AssertionError, match="bit-identical"):
-        assert_bf16_close("silu", bad, ref, max_ulp=MAX_ULP_SILU)
+        assert_bf16_close("silu", bad, ref, max_ulp=None)
 
 
 def test_silu_rows_read_early_fail(layer):
