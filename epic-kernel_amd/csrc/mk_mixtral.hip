@@ -77,12 +77,6 @@
 #define MK_PF_ROUNDS 1
 #endif
 
-// Opcode-5 items per wave warmed into L2 from opcode 8's prediction before
-// the O-proj wait (whole-model launches).
-#ifndef MK_SPEC_ITEMS
-#define MK_SPEC_ITEMS 1
-#endif
-
 // Dense VM: at most this many opcode-5 items (gate and up rows) staged in LDS
 // by the preceding opcode 4 (fewer when the LDS left over holds fewer).
 #ifndef MK_STAGE_ITEMS
@@ -190,8 +184,10 @@ struct KParams {
     // with argmax_out: the last workgroup also zeroes the barrier tensor (1)
     // and the logits (2) for the next launch
     int32_t reset_next;
-    // dense VM: opcode-5 items (gate and up rows) that opcode 4 stages in LDS
-    // while it waits, and where (u32x4 index into the dynamic LDS); 0: off
+    // opcode-5 items (gate and up rows) staged in LDS while a workgroup waits
+    // anyway -- dense VM: by opcode 4 or 5; Mixtral whole-model launches: by
+    // opcode 5, from opcode 8's prediction -- and where (u32x4 index into the
+    // dynamic LDS); 0: off
     int32_t stage_items;
     int32_t stage_off16;
     int32_t lds_bytes;  // dynamic LDS of the launch
@@ -927,12 +923,16 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
     // Speculative early loads (whole-model launches, the reference's
     // mx/rms_router_matvec.cu:259-290 re-expressed): once opcode 8 has
-    // predicted this layer's experts (checked, never waited for), each wave
-    // warms its first MK_SPEC_ITEMS items of the predicted top-1 expert into
-    // L2 (global_load_lds into an LDS sink: no registers held across the
-    // wait) before the O-proj wait.  A wrong prediction only costs the loads.
-    // More than one item per wave (128 KiB per CU, the CU's share of its
-    // XCD's L2) measured slower.
+    // predicted this layer's experts (checked, never waited for), waves 1 ..
+    // stage_items stream their first item of the predicted top-1 expert (a
+    // gate row and an up row) into LDS with global_load_lds while the
+    // workgroup waits for the O projection; if the routing then agrees, those
+    // items are computed from LDS.  A wrong prediction only costs the loads.
+    // Wave 0 stages nothing: thread 0 polls the counter, and a poll waits for
+    // every load its wave issued before it.  (Warming the same rows into L2
+    // instead gained nothing: 32 compute units x 128 KiB fill an XCD's 4 MiB
+    // L2, which the O projection streams through meanwhile.)
+    int staged = 0;  // items 1 .. staged of this instruction are in LDS (of expert spec_e[0])
     if constexpr (kSpec) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         if (threadIdx.x == 0) {
@@ -947,17 +947,21 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
         }
         __syncthreads();
         const int pe0 = __builtin_amdgcn_readfirstlane(sh.spec_e[0]);
-        if (pe0 >= 0) {
+        // (only in the 8-expert kernel: the expert-count-generic one would spill)
+        if (kE > 0 && pe0 >= 0) {
+            staged = min(p.stage_items, nrows - 1);
             stamp(tim, MK_TEVENT_FIRST_USE);
-            lds_void_t *sink = (lds_void_t *)(act + (lds_prefetch_offset(p) >> 4) + wave * 64);
-            const int nc = p.H / kChunkElems;
-            for (int it = wave; it < nrows && it < MK_SPEC_ITEMS * kWaves; it += kWaves) {
-                const size_t off = ((size_t)(layer * p.E + pe0) * p.F + row0 + it) * (size_t)p.H;
+            if (wave >= 1 && wave <= staged) {
+                const int nc = p.H / kChunkElems;
+                const size_t off = ((size_t)(layer * p.E + pe0) * p.F + row0 + wave) * (size_t)p.H;
                 const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
                 const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
+                u32x4 *dst = act + p.stage_off16 + (wave - 1) * 2 * nc * 64;
                 for (int i = 0; i < nc; ++i) {
-                    __builtin_amdgcn_global_load_lds((global_void_t *)(wg + i * 64), sink, 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds((global_void_t *)(wu + i * 64), sink, 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((global_void_t *)(wg + i * 64), (lds_void_t *)(dst + i * 64),
+                                                     16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((global_void_t *)(wu + i * 64),
+                                                     (lds_void_t *)(dst + (nc + i) * 64), 16, 0, 0);
                 }
             }
         }
@@ -1033,6 +1037,10 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
         // used: its SiLU store has then completed (a wait for it costs
         // nothing there), so no wave stops streaming to publish rows.
         const int total = __builtin_amdgcn_readfirstlane(sh.grp_first[K]);
+        // the staged items hold the predicted top-1 expert's rows: usable if
+        // the routing picked it first (items 0 .. nrows-1 are slot 0)
+        const bool from_lds = kSpec && kE > 0 && staged > 0 && wave >= 1 && wave <= staged &&
+                              __builtin_amdgcn_readfirstlane(sh.spec_e[0]) == t.i0;
         int k = 0, pending = -1;
         for (int it = wave; it < total; ++k) {
             int q = 0;
@@ -1043,9 +1051,21 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
             const int j = local >= nr;
             const int r = r0 + (j ? local - nr : local);
             const int e = j ? t.i1 : t.i0;
-            const size_t off = ((size_t)(layer * p.E + e) * p.F + r) * (size_t)p.H;
             float ag = 0.f, au = 0.f;
-            dot_pair(p.gate + off, p.up + off, act, act, p.H / kChunkElems, lane, ag, au);
+            if (kSpec && kE > 0 && k == 0 && from_lds) {
+                // this wave's own staged rows (its loads have landed: it has
+                // waited for its hidden-state loads since)
+                const int nc = p.H / kChunkElems;
+                const u32x4 *sg = act + p.stage_off16 + (wave - 1) * 2 * nc * 64 + lane, *su = sg + nc * 64;
+                __builtin_amdgcn_s_waitcnt(0);
+                for (int ch = 0; ch < nc; ++ch) {
+                    ag = dot8(sg[ch * 64], act[ch * 64 + lane], ag);
+                    au = dot8(su[ch * 64], act[ch * 64 + lane], au);
+                }
+            } else {
+                const size_t off = ((size_t)(layer * p.E + e) * p.F + r) * (size_t)p.H;
+                dot_pair(p.gate + off, p.up + off, act, act, p.H / kChunkElems, lane, ag, au);
+            }
             ag = wave_sum(ag);
             au = wave_sum(au);
             __builtin_amdgcn_s_waitcnt(0);
@@ -2451,37 +2471,38 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
 // Opcode 6 when the column chunk is all of F (matvec_reduction_size == F):
 // every row has one writer, so h = bf16(h + bf16(W[r] . silu)) is a plain
 // coherent read-modify-write in python_vm's order, with no atomics, and a
-// relaunch is bit-identical.  Rows [start, end) * down_proj_block_size in
-// batches of kRowBatch; an item is one full row (nc chunks, up to kSegChunks
-// loads per lane in flight), its sum kept in LDS until the batch ends; the
-// first item of each wave (its first kSegChunks chunks) is loaded before the
-// wait, and, when this
-// workgroup's opcode 5 already passed the O-proj wait (the residual rows are
-// final then), so are the first batch's residual rows.
+// relaunch is bit-identical.  An item is one full row of
+// [start, end) * down_proj_block_size (nc chunks, up to kSegChunks loads per
+// lane in flight), stored by its wave as soon as its sum is known, so only
+// the last item's store is outstanding at the end.  The first item of each
+// wave (its first kSegChunks chunks) is loaded before the wait, and, when
+// this workgroup's opcode 5 already passed the O-proj wait (the residual
+// rows are final then), so are the first kRowBatch residual rows.
 __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                 int32_t *tim, int layer, int b0, int b1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = b0 * p.down_bs, nrows = (b1 - b0) * p.down_bs;
     const int nc = p.F / kChunkElems;
     const uint16_t *wm = p.down + (size_t)layer * p.H * p.F;
-    const int first_batch = min(nrows, kRowBatch);
+    const int nearly = min(nrows, kRowBatch);  // rows whose residual is read before the wait
     RowRegs<kSegChunks> pre;  // up to a whole first row per wave (16 KiB), as many loads as a later item
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    if (wave < first_batch)
+    if (wave < nrows)
         load_row<kSegChunks>(pre, reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + wave) * p.F) + lane,
                              min(nc, kSegChunks));
     const bool hfinal = __builtin_amdgcn_readfirstlane(sh.route_layer) == layer;
     uint32_t hpre = 0;
-    if (hfinal && tid < first_batch) hpre = ld_dev16(p.hidden + r0 + tid);
+    if (hfinal && tid < nearly) hpre = ld_dev16(p.hidden + r0 + tid);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
+    uint32_t *hrow = reinterpret_cast<uint32_t *>(sh.part);  // the residual rows read early
+    if (hfinal && tid < nearly) hrow[tid] = hpre;
     for (int v = tid; v < (p.F >> 3); v += kThreads) act[v] = ld_dev128(p.silu, (uint32_t)v * 16u);
     __syncthreads();
-    float *part = sh.part;  // one fp32 sum per row of the batch
-    // the rest of row r0 + bb + it from chunk `done` on, added to acc
-    auto row_rest = [&](int bb, int it, int done, float acc) {
-        const u32x4 *w = reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + bb + it) * p.F) + lane;
+    // the rest of row r0 + it from chunk `done` on, added to acc
+    auto row_rest = [&](int it, int done, float acc) {
+        const u32x4 *w = reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + it) * p.F) + lane;
         while (done < nc) {
             const int n = min(nc - done, kSegChunks);
             RowRegs<kSegChunks> r;
@@ -2491,27 +2512,21 @@ __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &s
         }
         return acc;
     };
+    auto store_row = [&](int it, float acc) {  // lane 0
+        uint16_t *hp = p.hidden + r0 + it;
+        const uint32_t h = hfinal && it < nearly ? hrow[it] : ld_dev16(hp);
+        st_dev16(hp, f2bf(bf2f(h) + rbf(acc)));
+    };
     // the items loaded before the wait (outside the item loop, so their
     // registers are free again for the later items)
-    if (wave < first_batch) {
+    if (wave < nrows) {
         const int n = min(nc, kSegChunks);
-        const float acc = wave_sum(row_rest(0, wave, n, dot_row_regs<kSegChunks>(pre, act + lane, n, 0.f)));
-        if (lane == 0) part[wave] = acc;
+        const float acc = wave_sum(row_rest(wave, n, dot_row_regs<kSegChunks>(pre, act + lane, n, 0.f)));
+        if (lane == 0) store_row(wave, acc);
     }
-    for (int bb = 0; bb < nrows; bb += kRowBatch) {
-        const int nb_rows = min(kRowBatch, nrows - bb);
-        for (int it = bb == 0 ? next_local_item(sh, lane) : wave; it < nb_rows; it = next_local_item(sh, lane)) {
-            const float acc = wave_sum(row_rest(bb, it, 0, 0.f));
-            if (lane == 0) part[it] = acc;
-        }
-        __syncthreads();
-        for (int r = tid; r < nb_rows; r += kThreads) {
-            uint16_t *hp = p.hidden + r0 + bb + r;
-            const uint32_t h = hfinal && bb == 0 ? hpre : ld_dev16(hp);  // r == tid in the first batch
-            st_dev16(hp, f2bf(bf2f(h) + rbf(part[r])));
-        }
-        if (tid == 0) sh.next_item = kWaves;
-        __syncthreads();
+    for (int it = next_local_item(sh, lane); it < nrows; it = next_local_item(sh, lane)) {
+        const float acc = wave_sum(row_rest(it, 0, 0.f));
+        if (lane == 0) store_row(it, acc);
     }
     drain_and_sync();
     arrive(bar_at(p, layer, 6), b1 - b0);
@@ -3350,8 +3365,13 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
-    kp.stage_items = 0;
-    kp.stage_off16 = 0;
+    // whole-model launches: opcode 5 stages up to one predicted item per
+    // wave (but wave 0) in the LDS after the normed hidden state, within the
+    // launch's LDS (the opcode-2 ring makes it ~145 KiB at the Mixtral shape)
+    const size_t stage_off = (((size_t)g->hidden_size * 2 + 1023) / 1024) * 1024;
+    const size_t stage_item = (size_t)g->hidden_size * 4;
+    kp.stage_items = attn && lds > stage_off ? (int32_t)std::min((size_t)(kWaves - 1), (lds - stage_off) / stage_item) : 0;
+    kp.stage_off16 = (int32_t)(stage_off / 16);
     kp.lds_bytes = (int32_t)lds;
     kp.argmax_out = g->argmax_out;
     kp.next_embed = g->next_embed_weights;
