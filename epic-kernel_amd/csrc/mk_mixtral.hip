@@ -39,6 +39,7 @@
 
 #include <math.h>
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <stddef.h>
@@ -96,6 +97,15 @@ constexpr int kCachePolicySc1 = 16;     // buffer-load cache policy: device scop
 // Work-sharing scratch (int32): [0] exit counter, then a (cursor, done) pair
 // per instruction slot w * queue_len + q.
 constexpr int kScratchSlotBase = 16;
+// XCD relay (see wait_ge): 8 XCDs x kRelayEntries flags after a 128-byte
+// header; entry layer * kRelayOps + opcode - 1.  Counters of launches with
+// more layers or opcode rows are waited for without it.
+constexpr int kRelayXcds = 8;
+constexpr int kRelayLayers = 64;
+constexpr int kRelayOps = 16;
+constexpr int kRelayEntries = kRelayLayers * kRelayOps;
+constexpr size_t kRelayBytes = 128 + (size_t)kRelayXcds * kRelayEntries * 8;
+constexpr int kRelayGlobalEvery = 8;  // a waiter reads the counter itself every 8th poll
 constexpr int kPoolGroup = MK_POOL_GROUP;
 constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) that can be shared
 static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
@@ -197,6 +207,9 @@ struct KParams {
     // that are complete instead of waiting for the whole layer
     int32_t *chunk_ctr;
     int32_t scratch_clear;  // scratch ints from kScratchSlotBase the last workgroup zeroes
+    // XCD relay of barrier waits (NULL: off): word 0 is the launch epoch,
+    // then per XCD kRelayEntries 64-bit flags, one per (layer, opcode) counter
+    uint64_t *relay;
     AttnParams attn_params;  // read only through attn_of()
 };
 
@@ -233,6 +246,8 @@ struct SharedState {
     // most): first FFN row, rows, first pooled item, finished items
     int grp_row0[kMaxMerge], grp_nrows[kMaxMerge], grp_first[kMaxMerge + 1], grp_done[kMaxMerge];
     int ready_mask;  // opcode 6: column groups whose SiLU rows are complete
+    uint64_t *relay;     // this XCD's relay flags (NULL: off)
+    uint32_t relay_tag;  // this launch's flag tag (epoch + 1)
 };
 
 struct Ctx {
@@ -387,21 +402,74 @@ __device__ __forceinline__ void report_error(const KParams &p, int code, const C
     if (threadIdx.x == 0) report_error_lane(p, code, c, opcode, layer, expected, seen);
 }
 
+// L2-coherent accesses for the XCD relay flags: sc0 without sc1 misses the
+// compute unit's L1 but hits the XCD's L2, which every compute unit of the
+// XCD shares.  Inline assembly keeps the compiler from hoisting a poll out
+// of its loop; the load waits for its own result.
+__device__ __forceinline__ uint64_t ld_l2_u64(const uint64_t *p) {
+    uint64_t v;
+    asm volatile("global_load_dwordx2 %0, %1, off sc0\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ void st_l2_u64(uint64_t *p, uint64_t v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc0" : : "v"(p), "v"(v) : "memory");
+}
+
+// This XCD's relay flag for counter `ctr` (index 0 of a (layer, opcode)
+// row of the barrier tensor), or NULL.
+__device__ __forceinline__ uint64_t *relay_flag(const KParams &p, const SharedState &sh, const int32_t *ctr) {
+    if (sh.relay == nullptr) return nullptr;
+    const long off = ctr - p.bar;
+    if (off < 0 || off % p.bar_width != 0) return nullptr;
+    const long row = off / p.bar_width;
+    const int layer = (int)(row / p.bar_ops), op = (int)(row % p.bar_ops);
+    if (layer >= kRelayLayers || op >= kRelayOps) return nullptr;
+    return sh.relay + layer * kRelayOps + op;
+}
+
 // Wait until *ctr >= expected.  Thread 0 spins; the result is broadcast.
 // Returns false (uniformly) on time-out or when another worker has failed.
+//
+// Hundreds of workgroups polling one counter in HBM serialise on its memory
+// channel: a poll then takes microseconds, and the last waiter saw a
+// finished stage up to ~3 us after the first.  So the waiters of a layer
+// counter relay through their XCD's L2: each polls this XCD's flag for the
+// counter (an L2 hit), reads the counter itself only every
+// kRelayGlobalEvery-th poll, and the first to see it complete stores the
+// value into the flag for the other compute units of its XCD.  A flag
+// holds (launch tag, observed count); tags grow by one per launch, so a
+// flag left by an earlier launch never satisfies a wait.
 __device__ __forceinline__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int expected, const Ctx &c, int opcode,
                         int layer) {
     if (threadIdx.x == 0) {
         int ok = 1;
-        int v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (v < expected) {
+        uint64_t *flag = relay_flag(p, sh, ctr);
+        const uint32_t tag = sh.relay_tag;
+        auto flag_done = [&]() {
+            const uint64_t f = ld_l2_u64(flag);
+            return (uint32_t)(f >> 32) == tag && (int)(uint32_t)f >= expected;
+        };
+        bool done = flag != nullptr && flag_done();
+        int v = 0;
+        if (!done) {
+            v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            done = v >= expected;
+        }
+        if (!done) {
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             int nap = 1;
-            for (;;) {
+            for (int it = 1;; ++it) {
                 for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
                 if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
+                if (flag != nullptr) {
+                    if (flag_done()) break;
+                    if (it % kRelayGlobalEvery != 0) continue;
+                }
                 v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (v >= expected) break;
+                if (v >= expected) {
+                    if (flag != nullptr) st_l2_u64(flag, ((uint64_t)tag << 32) | (uint32_t)v);
+                    break;
+                }
                 if (aborted(p)) {
                     ok = 0;
                     break;
@@ -1703,6 +1771,24 @@ __device__ __forceinline__ float group_sum(float v, int G) {
     return v;
 }
 
+// The value lane l ^ o holds, for o in {8, 16, 32} (wave-uniform o): one
+// VALU operation each instead of an LDS permute -- DPP row_ror:8 within a
+// row of 16 lanes, and gfx950's v_permlane16_swap / v_permlane32_swap
+// across rows (applied to a register and its copy, the second result holds,
+// in the lanes below the swapped boundary, the partner rows' values).
+__device__ __forceinline__ float lane_xor(float v, int o, int lane) {
+    const uint32_t u = __float_as_uint(v);
+    if (o == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __uint_as_float(lane < 32 ? r[1] : r[0]);
+    }
+    if (o == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __uint_as_float((lane & 16) == 0 ? r[1] : r[0]);
+    }
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, (int)u, 0x128, 0xf, 0xf, false));  // row_ror:8
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Scores are kept in log2 units: q is pre-scaled by attn_scale * log2(e), so
@@ -1904,16 +1990,22 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, Shared
     // fold the token slots of the wave (lanes with the same dp) to the wave max
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
+        // partners at lane distance 8 (head dim 64 only), 16 and 32
         float mw = M[h];
-        for (int o = G; o < 64; o <<= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
+        if (G == 8) mw = fmaxf(mw, lane_xor(mw, 8, lane));
+        mw = fmaxf(mw, lane_xor(mw, 16, lane));
+        mw = fmaxf(mw, lane_xor(mw, 32, lane));
         const float f = M[h] == -INFINITY ? 0.f : exp2_fast(M[h] - mw);
         L[h] *= f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] *= f;
-        for (int o = G; o < 64; o <<= 1) {
-            L[h] += __shfl_xor(L[h], o);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] += __shfl_xor(acc[h][j], o);
+        for (int k = 0; k < 3; ++k) {
+            const int o = 8 << k;
+            if (o < G) continue;
+            L[h] += lane_xor(L[h], o, lane);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] += lane_xor(acc[h][j], o, lane);
         }
         M[h] = mw;
     }
@@ -2706,6 +2798,25 @@ __device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
     }
 }
 
+// Per-workgroup set-up at kernel start: no routing or staging yet; the
+// XCD relay region of this compute unit's XCD (hardware register XCC_ID)
+// and the launch tag, the epoch every workgroup reads before any of them
+// can have exited (the last one to exit advances it) plus one.
+__device__ __forceinline__ void kernel_enter(const KParams &p, SharedState &sh) {
+    if (threadIdx.x == 0) {
+        sh.route_layer = -1;
+        sh.stage_slot = -1;
+        sh.relay = nullptr;
+        sh.relay_tag = 0;
+        if (p.relay != nullptr) {
+            const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)) % kRelayXcds;
+            sh.relay = p.relay + 16 + (size_t)xcc * kRelayEntries;
+            sh.relay_tag = ld_dev32(p.relay) + 1u;
+        }
+    }
+    __syncthreads();
+}
+
 // Zero n 32-bit words at p (4-byte aligned) with the workgroup: 16-byte
 // stores from the first 16-byte boundary on.
 __device__ __forceinline__ void zero_words(uint32_t *p, size_t n) {
@@ -2742,6 +2853,8 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
         }
         // work-sharing cursors, then the column-chunk counters
         for (int i = threadIdx.x; i < p.scratch_clear; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
+        // the next launch's relay tag
+        if (p.relay != nullptr && threadIdx.x == 0) st_dev32(p.relay, sh.relay_tag);
         drain_and_sync();
         if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -2751,11 +2864,7 @@ template <int kE, bool kAttn>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
-    if (threadIdx.x == 0) {
-        sh.route_layer = -1;
-        sh.stage_slot = -1;
-    }
-    __syncthreads();
+    kernel_enter(p, sh);
 
     const int w = blockIdx.x;
     for (int q = 0; q < p.queue_len; ++q) {
@@ -2809,11 +2918,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
 __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
-    if (threadIdx.x == 0) {
-        sh.route_layer = -1;
-        sh.stage_slot = -1;
-    }
-    __syncthreads();
+    kernel_enter(p, sh);
 
     const int w = blockIdx.x;
     for (int q = 0; q < p.queue_len; ++q) {
@@ -2869,6 +2974,10 @@ struct DeviceState {
     bool launched = false;
     hipStream_t last_stream = nullptr;
     hipEvent_t order_event = nullptr;
+    // XCD relay flags and the launch epoch (kRelayBytes, zeroed), allocated
+    // with the status words and kept until the process ends, so the epoch
+    // only ever grows
+    uint64_t *relay = nullptr;
 };
 
 std::mutex g_mutex;
@@ -2895,6 +3004,10 @@ int device_state(int dev, DeviceState **out) {
         e = hipMalloc(reinterpret_cast<void **>(&st.status), MK_STATUS_WORDS * sizeof(int32_t));
         if (e != hipSuccess) return hip_fail(e, "hipMalloc");
         e = hipMemset(st.status, 0, MK_STATUS_WORDS * sizeof(int32_t));
+        if (e != hipSuccess) return hip_fail(e, "hipMemset");
+        e = hipMalloc(reinterpret_cast<void **>(&st.relay), kRelayBytes);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+        e = hipMemset(st.relay, 0, kRelayBytes);
         if (e != hipSuccess) return hip_fail(e, "hipMemset");
         st.ready = true;
     }
@@ -2985,6 +3098,16 @@ int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t l
     st->launched = true;
     st->last_stream = stream;
     return MK_OK;
+}
+
+// The relay region for a launch, or NULL: when its counters do not all fit
+// the region, or when MK_XCD_RELAY=0 in the environment (a measurement
+// switch: every waiter then polls the counter in HBM itself).
+uint64_t *relay_for(const DeviceState *st, int64_t layers, int64_t bar_ops) {
+    if (layers > kRelayLayers || bar_ops > kRelayOps) return nullptr;
+    const char *env = std::getenv("MK_XCD_RELAY");
+    if (env != nullptr && env[0] == '0') return nullptr;
+    return st->relay;
 }
 
 uint32_t timeout_ticks(uint32_t spin_timeout_us) {
@@ -3193,6 +3316,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
 
     KParams kp{};
     kp.chunk_ctr = nullptr;
+    kp.relay = relay_for(st, g->num_layers, g->bar_ops);
     kp.scratch_clear = (int32_t)(2 * (size_t)g->num_workers * (size_t)g->queue_len);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
@@ -3331,6 +3455,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
 
     KParams kp;
     kp.chunk_ctr = overlap ? st->scratch + kScratchSlotBase + cursors : nullptr;
+    kp.relay = relay_for(st, g->num_layers, g->bar_ops);
     kp.scratch_clear = (int32_t)(cursors + chunks);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
