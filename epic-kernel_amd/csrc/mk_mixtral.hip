@@ -97,15 +97,14 @@ constexpr int kCachePolicySc1 = 16;     // buffer-load cache policy: device scop
 // Work-sharing scratch (int32): [0] exit counter, then a (cursor, done) pair
 // per instruction slot w * queue_len + q.
 constexpr int kScratchSlotBase = 16;
-// XCD relay (see wait_ge): 8 XCDs x kRelayEntries flags after a 128-byte
-// header; entry layer * kRelayOps + opcode - 1.  Counters of launches with
-// more layers or opcode rows are waited for without it.
-constexpr int kRelayXcds = 8;
-constexpr int kRelayLayers = 64;
-constexpr int kRelayOps = 16;
-constexpr int kRelayEntries = kRelayLayers * kRelayOps;
-constexpr size_t kRelayBytes = 128 + (size_t)kRelayXcds * kRelayEntries * 8;
-constexpr int kRelayGlobalEvery = 8;  // a waiter reads the counter itself every 8th poll
+// Spread layer counters: arrivals on the counter at index 0 of a (layer,
+// opcode) row of the barrier tensor go to one of kSpread counters in
+// library scratch instead (the arriving workgroup's XCD picks it, blocks
+// spreading over XCDs round-robin), kSpreadAlign ints apart; waiters add the
+// row-0 counter and its kSpread parts, and the last workgroup of the launch
+// folds the parts back into the barrier tensor.
+constexpr int kSpread = 8;
+constexpr int kSpreadAlign = 1024;
 constexpr int kPoolGroup = MK_POOL_GROUP;
 constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) that can be shared
 static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
@@ -207,9 +206,10 @@ struct KParams {
     // that are complete instead of waiting for the whole layer
     int32_t *chunk_ctr;
     int32_t scratch_clear;  // scratch ints from kScratchSlotBase the last workgroup zeroes
-    // XCD relay of barrier waits (NULL: off): word 0 is the launch epoch,
-    // then per XCD kRelayEntries 64-bit flags, one per (layer, opcode) counter
-    uint64_t *relay;
+    // spread layer counters (NULL: off): kSpread parts of spread_rows
+    // (layer, opcode) rows, spread_stride ints apart
+    int32_t *spread;
+    int32_t spread_rows, spread_stride;
     AttnParams attn_params;  // read only through attn_of()
 };
 
@@ -246,8 +246,6 @@ struct SharedState {
     // most): first FFN row, rows, first pooled item, finished items
     int grp_row0[kMaxMerge], grp_nrows[kMaxMerge], grp_first[kMaxMerge + 1], grp_done[kMaxMerge];
     int ready_mask;  // opcode 6: column groups whose SiLU rows are complete
-    uint64_t *relay;     // this XCD's relay flags (NULL: off)
-    uint32_t relay_tag;  // this launch's flag tag (epoch + 1)
 };
 
 struct Ctx {
@@ -402,74 +400,73 @@ __device__ __forceinline__ void report_error(const KParams &p, int code, const C
     if (threadIdx.x == 0) report_error_lane(p, code, c, opcode, layer, expected, seen);
 }
 
-// L2-coherent accesses for the XCD relay flags: sc0 without sc1 misses the
-// compute unit's L1 but hits the XCD's L2, which every compute unit of the
-// XCD shares.  Inline assembly keeps the compiler from hoisting a poll out
-// of its loop; the load waits for its own result.
-__device__ __forceinline__ uint64_t ld_l2_u64(const uint64_t *p) {
-    uint64_t v;
-    asm volatile("global_load_dwordx2 %0, %1, off sc0\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+// Row of the spread counter table for `ctr` (the counter at index 0 of a
+// (layer, opcode) row of the barrier tensor), or -1 (not spread).
+__device__ __forceinline__ int spread_row(const KParams &p, const int32_t *ctr) {
+    if (p.spread == nullptr) return -1;
+    const long off = ctr - p.bar;
+    if (off < 0 || off % p.bar_width != 0) return -1;
+    const long row = off / p.bar_width;
+    return row < p.spread_rows ? (int)row : -1;
+}
+
+// One lane adds n arrivals to counter `ctr`.  A few hundred workgroups that
+// finish a stage together all add to one address, and the memory channel
+// applies those atomics one at a time (~15 ns each): the last of 256
+// O-projection arrivals landed ~4 us after the stage ended.  A spread
+// counter's arrivals go to this XCD's part instead, 32 per part.
+__device__ __forceinline__ void arrive_add(const KParams &p, int32_t *ctr, int n) {
+    const int row = spread_row(p, ctr);
+    int32_t *dst = row < 0 ? ctr : p.spread + (size_t)(blockIdx.x % kSpread) * p.spread_stride + row;
+    __hip_atomic_fetch_add(dst, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void arrive(const KParams &p, int32_t *ctr, int n) {
+    if (threadIdx.x == 0) arrive_add(p, ctr, n);
+}
+
+// Current value of counter `ctr` (row `row` of the spread table, or -1),
+// read by one lane: the counter and its kSpread parts, all loads in flight
+// together.
+__device__ __forceinline__ int counter_value(const KParams &p, const int32_t *ctr, int row) {
+    int v = (int)ld_dev32(ctr);
+    if (row >= 0) {
+        uint32_t part[kSpread];
+#pragma unroll
+        for (int k = 0; k < kSpread; ++k) part[k] = ld_dev32(p.spread + (size_t)k * p.spread_stride + row);
+#pragma unroll
+        for (int k = 0; k < kSpread; ++k) v += (int)part[k];
+    }
     return v;
 }
-__device__ __forceinline__ void st_l2_u64(uint64_t *p, uint64_t v) {
-    asm volatile("global_store_dwordx2 %0, %1, off sc0" : : "v"(p), "v"(v) : "memory");
+
+// Whether counter `ctr` has reached `expected`, for the workgroup (thread 0
+// reads it; ends with a workgroup barrier).
+__device__ __forceinline__ bool counter_reached(const KParams &p, SharedState &sh, const int32_t *ctr, int expected) {
+    if (threadIdx.x == 0) sh.flag = counter_value(p, ctr, spread_row(p, ctr)) >= expected;
+    __syncthreads();
+    const bool r = sh.flag != 0;
+    __syncthreads();
+    return r;
 }
 
-// This XCD's relay flag for counter `ctr` (index 0 of a (layer, opcode)
-// row of the barrier tensor), or NULL.
-__device__ __forceinline__ uint64_t *relay_flag(const KParams &p, const SharedState &sh, const int32_t *ctr) {
-    if (sh.relay == nullptr) return nullptr;
-    const long off = ctr - p.bar;
-    if (off < 0 || off % p.bar_width != 0) return nullptr;
-    const long row = off / p.bar_width;
-    const int layer = (int)(row / p.bar_ops), op = (int)(row % p.bar_ops);
-    if (layer >= kRelayLayers || op >= kRelayOps) return nullptr;
-    return sh.relay + layer * kRelayOps + op;
-}
-
-// Wait until *ctr >= expected.  Thread 0 spins; the result is broadcast.
-// Returns false (uniformly) on time-out or when another worker has failed.
-//
-// Hundreds of workgroups polling one counter in HBM serialise on its memory
-// channel: a poll then takes microseconds, and the last waiter saw a
-// finished stage up to ~3 us after the first.  So the waiters of a layer
-// counter relay through their XCD's L2: each polls this XCD's flag for the
-// counter (an L2 hit), reads the counter itself only every
-// kRelayGlobalEvery-th poll, and the first to see it complete stores the
-// value into the flag for the other compute units of its XCD.  A flag
-// holds (launch tag, observed count); tags grow by one per launch, so a
-// flag left by an earlier launch never satisfies a wait.
+// Wait until counter `ctr` >= expected.  Thread 0 spins; the result is
+// broadcast.  Returns false (uniformly) on time-out or when another worker
+// has failed.
 __device__ __forceinline__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int expected, const Ctx &c, int opcode,
                         int layer) {
     if (threadIdx.x == 0) {
+        const int row = spread_row(p, ctr);
         int ok = 1;
-        uint64_t *flag = relay_flag(p, sh, ctr);
-        const uint32_t tag = sh.relay_tag;
-        auto flag_done = [&]() {
-            const uint64_t f = ld_l2_u64(flag);
-            return (uint32_t)(f >> 32) == tag && (int)(uint32_t)f >= expected;
-        };
-        bool done = flag != nullptr && flag_done();
-        int v = 0;
-        if (!done) {
-            v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            done = v >= expected;
-        }
-        if (!done) {
+        int v = counter_value(p, ctr, row);
+        if (v < expected) {
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             int nap = 1;
-            for (int it = 1;; ++it) {
+            for (;;) {
                 for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
                 if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
-                if (flag != nullptr) {
-                    if (flag_done()) break;
-                    if (it % kRelayGlobalEvery != 0) continue;
-                }
-                v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (v >= expected) {
-                    if (flag != nullptr) st_l2_u64(flag, ((uint64_t)tag << 32) | (uint32_t)v);
-                    break;
-                }
+                v = counter_value(p, ctr, row);
+                if (v >= expected) break;
                 if (aborted(p)) {
                     ok = 0;
                     break;
@@ -495,11 +492,6 @@ __device__ __forceinline__ void drain_and_sync() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 }
-
-__device__ __forceinline__ void arrive(int32_t *ctr, int n) {
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 
 // ---------------------------------------------------------------------------
 // GEMV core: two rows at once, N chunks of 512 columns each
@@ -858,9 +850,7 @@ __device__ __forceinline__ void publish_items(const KParams &p, int32_t *done, i
     __builtin_amdgcn_s_waitcnt(0);
     if (lane == 0) {
         const int prev = __hip_atomic_fetch_add(done, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (prev + n == items + 1)
-            __hip_atomic_fetch_add(bar_at(p, layer, 5), nrows / p.expert_bs, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        if (prev + n == items + 1) arrive_add(p, bar_at(p, layer, 5), nrows / p.expert_bs);
     }
 }
 
@@ -900,7 +890,7 @@ __device__ __forceinline__ void upgate_item_done(const KParams &p, SharedState &
     if (lane != 0 || k < 0) return;
     const int r0 = sh.grp_row0[k], n = sh.grp_nrows[k];
     if (atomicAdd(&sh.grp_done[k], 1) + 1 != 2 * n) return;
-    __hip_atomic_fetch_add(bar_at(p, layer, 5), n / p.expert_bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrive_add(p, bar_at(p, layer, 5), n / p.expert_bs);
     if (p.chunk_ctr != nullptr) {
         int32_t *cc = p.chunk_ctr + (size_t)layer * (p.F / kChunkElems);
         for (int r = r0; r < r0 + n;) {
@@ -1003,9 +993,10 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     int staged = 0;  // items 1 .. staged of this instruction are in LDS (of expert spec_e[0])
     if constexpr (kSpec) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const bool predicted = !p.work_sharing && counter_reached(p, sh, bar_at(p, layer, 8), 1);
         if (threadIdx.x == 0) {
             int e0 = -1, e1 = -1;
-            if (!p.work_sharing && (int)ld_dev32(bar_at(p, layer, 8)) >= 1) {
+            if (predicted) {
                 e0 = (int)ld_dev32(p.pred_idx);
                 e1 = (int)ld_dev32(p.pred_idx + 1);
                 if (e0 < 0 || e0 >= p.E || e1 < 0 || e1 >= p.E) e0 = e1 = -1;
@@ -1362,7 +1353,7 @@ __device__ __forceinline__ bool downproj_overlapped(const KParams &p, SharedStat
         st_dev16(p.hidden + row0 + r, f2bf(h));
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 6), 2 * (end - start));
+    arrive(p, bar_at(p, layer, 6), 2 * (end - start));
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -1419,10 +1410,7 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
     // Infinity Cache.  Workgroups that arrive after the last producer skip
     // it.
     if (known) {
-        if (tid == 0) sh.flag = (int)ld_dev32(ready) < expected;
-        __syncthreads();
-        const bool warm = sh.flag != 0;
-        __syncthreads();
+        const bool warm = !counter_reached(p, sh, ready, expected);
         if (warm) {
             __attribute__((address_space(3))) void *sink =
                 (__attribute__((address_space(3))) void *)(act + (lds_prefetch_offset(p) >> 4) + wave * 64);
@@ -1504,7 +1492,7 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
         __syncthreads();
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 6), 2 * (end - start));
+    arrive(p, bar_at(p, layer, 6), 2 * (end - start));
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -1537,7 +1525,7 @@ __device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u3
         st_dev32(p.pred_idx + 1, (uint32_t)t.i1);
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 8), 1);
+    arrive(p, bar_at(p, layer, 8), 1);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -2054,7 +2042,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, Shared
     }
     drain_and_sync();
     if (a.skip_red)
-        arrive(bar_at(p, layer, 3), GQA);
+        arrive(p, bar_at(p, layer, 3), GQA);
     else if (threadIdx.x < GQA)
         __hip_atomic_fetch_add(bar_at(p, layer, 2) + h0 + threadIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
@@ -2151,7 +2139,7 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
         }
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 3), gqa);
+    arrive(p, bar_at(p, layer, 3), gqa);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -2222,11 +2210,8 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     // The residual rows of each wave's first item are final once the
     // previous layer's down-projection is complete (or at layer 0): read
     // them now instead of after the sums (one dependent load less).
-    if (threadIdx.x == 0)
-        sh.flag = layer == 0 || (int)ld_dev32(bar_at(p, layer - 1, 6)) >= p.down_arrivals;
-    __syncthreads();
-    const bool hfinal = sh.flag != 0 && 2 * wave < nrows;  // uniform
-    __syncthreads();
+    const bool hfinal = (layer == 0 || counter_reached(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals)) &&
+                        2 * wave < nrows;  // uniform
     const int rpre = r0 + 2 * wave;
     uint32_t hpair = 0;
     if (hfinal && lane == 0) hpair = ld_dev32(p.hidden + rpre);
@@ -2247,7 +2232,7 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
         st_dev16(hp, f2bf(bf2f(h) + rbf(s)));
     });
     drain_and_sync();
-    arrive(bar_at(p, layer, 4), b1 - b0);
+    arrive(p, bar_at(p, layer, 4), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -2492,7 +2477,7 @@ __device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &s
         upgate_item(p, act, layer, row, 1, 0, 0, 0, lane);
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 5), n);
+    arrive(p, bar_at(p, layer, 5), n);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -2555,7 +2540,7 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
         }
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 6), b1 - b0);
+    arrive(p, bar_at(p, layer, 6), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -2621,7 +2606,7 @@ __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &s
         if (lane == 0) store_row(it, acc);
     }
     drain_and_sync();
-    arrive(bar_at(p, layer, 6), b1 - b0);
+    arrive(p, bar_at(p, layer, 6), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -2798,25 +2783,6 @@ __device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
     }
 }
 
-// Per-workgroup set-up at kernel start: no routing or staging yet; the
-// XCD relay region of this compute unit's XCD (hardware register XCC_ID)
-// and the launch tag, the epoch every workgroup reads before any of them
-// can have exited (the last one to exit advances it) plus one.
-__device__ __forceinline__ void kernel_enter(const KParams &p, SharedState &sh) {
-    if (threadIdx.x == 0) {
-        sh.route_layer = -1;
-        sh.stage_slot = -1;
-        sh.relay = nullptr;
-        sh.relay_tag = 0;
-        if (p.relay != nullptr) {
-            const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)) % kRelayXcds;
-            sh.relay = p.relay + 16 + (size_t)xcc * kRelayEntries;
-            sh.relay_tag = ld_dev32(p.relay) + 1u;
-        }
-    }
-    __syncthreads();
-}
-
 // Zero n 32-bit words at p (4-byte aligned) with the workgroup: 16-byte
 // stores from the first 16-byte boundary on.
 __device__ __forceinline__ void zero_words(uint32_t *p, size_t n) {
@@ -2841,6 +2807,23 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
     __syncthreads();
     if (sh.flag) {
         if (p.argmax_out != nullptr && p.attn && !aborted(p)) exit_argmax(p, sh);
+        // spread counters: their parts back into the barrier tensor (which
+        // then holds what the reference's counters would), parts zeroed
+        if (p.spread != nullptr) {
+            for (int row = threadIdx.x; row < p.spread_rows; row += kThreads) {
+                int sum = 0;
+#pragma unroll
+                for (int k = 0; k < kSpread; ++k) {
+                    int32_t *q = p.spread + (size_t)k * p.spread_stride + row;
+                    sum += (int)ld_dev32(q);
+                    st_dev32(q, 0u);
+                }
+                if (sum != 0 && p.reset_next == 0) {
+                    int32_t *b = p.bar + (size_t)row * p.bar_width;
+                    st_dev32(b, ld_dev32(b) + (uint32_t)sum);
+                }
+            }
+        }
         if (p.reset_next > 0) {
             // every other workgroup is done with the barriers, and the
             // argmax above has read the logits
@@ -2853,8 +2836,6 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
         }
         // work-sharing cursors, then the column-chunk counters
         for (int i = threadIdx.x; i < p.scratch_clear; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
-        // the next launch's relay tag
-        if (p.relay != nullptr && threadIdx.x == 0) st_dev32(p.relay, sh.relay_tag);
         drain_and_sync();
         if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -2864,7 +2845,11 @@ template <int kE, bool kAttn>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
-    kernel_enter(p, sh);
+    if (threadIdx.x == 0) {
+        sh.route_layer = -1;
+        sh.stage_slot = -1;
+    }
+    __syncthreads();
 
     const int w = blockIdx.x;
     for (int q = 0; q < p.queue_len; ++q) {
@@ -2918,7 +2903,11 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
 __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
-    kernel_enter(p, sh);
+    if (threadIdx.x == 0) {
+        sh.route_layer = -1;
+        sh.stage_slot = -1;
+    }
+    __syncthreads();
 
     const int w = blockIdx.x;
     for (int q = 0; q < p.queue_len; ++q) {
@@ -2974,10 +2963,6 @@ struct DeviceState {
     bool launched = false;
     hipStream_t last_stream = nullptr;
     hipEvent_t order_event = nullptr;
-    // XCD relay flags and the launch epoch (kRelayBytes, zeroed), allocated
-    // with the status words and kept until the process ends, so the epoch
-    // only ever grows
-    uint64_t *relay = nullptr;
 };
 
 std::mutex g_mutex;
@@ -3004,10 +2989,6 @@ int device_state(int dev, DeviceState **out) {
         e = hipMalloc(reinterpret_cast<void **>(&st.status), MK_STATUS_WORDS * sizeof(int32_t));
         if (e != hipSuccess) return hip_fail(e, "hipMalloc");
         e = hipMemset(st.status, 0, MK_STATUS_WORDS * sizeof(int32_t));
-        if (e != hipSuccess) return hip_fail(e, "hipMemset");
-        e = hipMalloc(reinterpret_cast<void **>(&st.relay), kRelayBytes);
-        if (e != hipSuccess) return hip_fail(e, "hipMalloc");
-        e = hipMemset(st.relay, 0, kRelayBytes);
         if (e != hipSuccess) return hip_fail(e, "hipMemset");
         st.ready = true;
     }
@@ -3100,14 +3081,24 @@ int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t l
     return MK_OK;
 }
 
-// The relay region for a launch, or NULL: when its counters do not all fit
-// the region, or when MK_XCD_RELAY=0 in the environment (a measurement
-// switch: every waiter then polls the counter in HBM itself).
-uint64_t *relay_for(const DeviceState *st, int64_t layers, int64_t bar_ops) {
-    if (layers > kRelayLayers || bar_ops > kRelayOps) return nullptr;
-    const char *env = std::getenv("MK_XCD_RELAY");
-    if (env != nullptr && env[0] == '0') return nullptr;
-    return st->relay;
+// Spread-counter layout of a launch (scratch ints): the parts follow the
+// cursors and column-chunk counters, kSpreadAlign-aligned.  MK_SPREAD=0 in
+// the environment turns them off (a measurement switch: every arrival then
+// goes to the barrier tensor itself).
+struct SpreadLayout {
+    bool on;
+    size_t offset, rows, stride, end;
+};
+
+SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops) {
+    SpreadLayout s{};
+    const char *env = std::getenv("MK_SPREAD");
+    s.on = env == nullptr || env[0] != '0';
+    s.rows = (size_t)layers * (size_t)bar_ops;
+    s.stride = (s.rows + kSpreadAlign - 1) / kSpreadAlign * kSpreadAlign;
+    s.offset = (used + kSpreadAlign - 1) / kSpreadAlign * kSpreadAlign;
+    s.end = s.on ? s.offset + (size_t)kSpread * s.stride : used;
+    return s;
 }
 
 uint32_t timeout_ticks(uint32_t spin_timeout_us) {
@@ -3311,12 +3302,16 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     const size_t stage_items =
         lds_cap > stage_off ? std::min((size_t)MK_STAGE_ITEMS, (lds_cap - stage_off) / stage_item) : 0;
     if (stage_items > 0) lds = std::max(lds, stage_off + stage_items * stage_item);
-    rc = ensure_scratch(st, kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len);
+    const SpreadLayout sp = spread_layout(kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len,
+                                          g->num_layers, g->bar_ops);
+    rc = ensure_scratch(st, sp.end);
     if (rc != MK_OK) return rc;
 
     KParams kp{};
     kp.chunk_ctr = nullptr;
-    kp.relay = relay_for(st, g->num_layers, g->bar_ops);
+    kp.spread = sp.on ? st->scratch + sp.offset : nullptr;
+    kp.spread_rows = (int32_t)sp.rows;
+    kp.spread_stride = (int32_t)sp.stride;
     kp.scratch_clear = (int32_t)(2 * (size_t)g->num_workers * (size_t)g->queue_len);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
@@ -3450,12 +3445,15 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const bool overlap = g->downproj_overlap != 0 && !g->work_sharing && g->num_experts == 8 &&
                          g->qkv_weights == nullptr;
     const size_t chunks = overlap ? (size_t)g->num_layers * (size_t)(g->intermediate_size / 512) : 0;
-    rc = ensure_scratch(st, kScratchSlotBase + cursors + chunks);
+    const SpreadLayout sp = spread_layout(kScratchSlotBase + cursors + chunks, g->num_layers, g->bar_ops);
+    rc = ensure_scratch(st, sp.end);
     if (rc != MK_OK) return rc;
 
     KParams kp;
     kp.chunk_ctr = overlap ? st->scratch + kScratchSlotBase + cursors : nullptr;
-    kp.relay = relay_for(st, g->num_layers, g->bar_ops);
+    kp.spread = sp.on ? st->scratch + sp.offset : nullptr;
+    kp.spread_rows = (int32_t)sp.rows;
+    kp.spread_stride = (int32_t)sp.stride;
     kp.scratch_clear = (int32_t)(cursors + chunks);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
