@@ -305,7 +305,8 @@ def decode_bench(args, config: str, steps: int, warmup: int):
         gkw[k] = int(v)
     gen = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                              dag_kwargs=None if llama else {"predict": not args.no_predict},
-                             device_argmax=not args.host_argmax, reset_next=not args.no_reset)
+                             device_argmax=not args.host_argmax, reset_next=not args.no_reset,
+                             late_loads=args.late_loads)
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
@@ -327,6 +328,7 @@ def decode_bench(args, config: str, steps: int, warmup: int):
         rec = TimingRecord.from_globals(g0)
         save_record(args.trace, rec)
         print(format_report(rec), file=sys.stderr, flush=True)
+    ab = prefetch_ab(args, gen, model, prefill, steps, llama, gkw) if args.prefetch_ab else None
     ms = secs / steps * 1e3
     nbytes = (decode_bytes_per_token_llama if llama else decode_bytes_per_token)(cfg, prefill + steps // 2)
     kernel_s = gpu_s / steps
@@ -367,6 +369,7 @@ def decode_bench(args, config: str, steps: int, warmup: int):
                             if hasattr(g, k)},
             "partition_policy": args.partitions,
             "argmax": "torch, between launches" if args.host_argmax else "in-kernel, with the next embedding",
+            "late_loads": args.late_loads,
             "fills_between_launches": args.host_argmax or args.no_reset,
         },
         "ms_per_step_hip_events": kernel_s * 1e3,
@@ -387,7 +390,63 @@ def decode_bench(args, config: str, steps: int, warmup: int):
         },
         "tokens_tail": tokens[0, -8:].tolist(),
     }
+    if ab is not None:
+        out["prefetch_ab"] = ab
     return out, model, gen
+
+
+def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: dict):
+    """Prefetch on vs off in the same process, alternating for
+    ``args.prefetch_ab`` rounds of ``steps`` decode steps each (medians of
+    HIP-event tokens/s): "on" is the default launch; "late_loads" waits for
+    every instruction's inputs before any of its loads and stages nothing
+    ahead (every early load and all LDS staging off); for the Mixtral shape,
+    "no_predict" also leaves out opcode 8 and the predicted-expert staging
+    that uses it (the rest of the early loads on).  The reference credits
+    its L2 prefetch of next-iteration weights with +5-8 % on Llama-3B
+    decode (README.md:13, B200; demos/low-latency-llama/
+    matvec_pipeline.cuh:217-233)."""
+    import statistics
+
+    import torch
+
+    from megakernels_amd.mixtral.generate import MK_Generator
+
+    base = {"device_argmax": not args.host_argmax, "reset_next": not args.no_reset}
+    variants = {"on": gen}
+    variants["late_loads"] = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
+                                                dag_kwargs=None if llama else {"predict": not args.no_predict},
+                                                late_loads=True, **base)
+    if not llama:
+        variants["no_predict"] = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
+                                                    dag_kwargs={"predict": False}, **base)
+    rates = {k: [] for k in variants}
+    for r in range(args.prefetch_ab):
+        for name, g in variants.items():
+            g.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=1)
+            rates[name].append(steps / g.last_gpu_seconds)
+        print(f"bench: prefetch A/B round {r}: " + ", ".join(f"{k} {v[-1]:.1f}" for k, v in rates.items()),
+              file=sys.stderr, flush=True)
+    import mk_mixtral
+
+    mk_mixtral.raise_if_failed("cuda")
+    med = {k: statistics.median(v) for k, v in rates.items()}
+    out = {
+        "rounds": args.prefetch_ab,
+        "steps_per_round": steps,
+        "tokens_per_s": {k: round(v, 2) for k, v in med.items()},
+        "all": {k: [round(x, 2) for x in v] for k, v in rates.items()},
+        "gain_on_vs_late_loads": med["on"] / med["late_loads"] - 1.0,
+        "reference": "+5-8 % from L2 prefetch on Llama-3B decode (README.md:13, NVIDIA B200)",
+        "unit": "tokens/s by HIP events, median over rounds",
+    }
+    if "no_predict" in med:
+        out["gain_on_vs_no_predict"] = med["on"] / med["no_predict"] - 1.0
+    for name in list(variants):
+        if name != "on":
+            del variants[name]
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline_decode(model, prefill: int, seconds: float, threads: int, sm_count: int, layers: int = 2):
@@ -605,6 +664,12 @@ def main():
                     help="c4/c5: leave out opcode 8 (expert prediction) and the early expert loads that use it")
     ap.add_argument("--predict-sigma", type=float, default=None,
                     help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
+    ap.add_argument("--late-loads", action="store_true",
+                    help="c3/c4/c5: prefetch off -- every instruction waits for its inputs before any of its "
+                         "loads, nothing is staged ahead in LDS")
+    ap.add_argument("--prefetch-ab", type=int, default=3, metavar="ROUNDS",
+                    help="c3/c4/c5: after the timed run, ROUNDS alternating rounds of prefetch on / late loads "
+                         "(/ no predictor, Mixtral) in the same process, reported as prefetch_ab (0: skip)")
     ap.add_argument("--host-argmax", action="store_true",
                     help="c3/c4/c5: torch.argmax and the embedding lookup between launches, as the reference's "
                          "generator (default: inside the launch)")

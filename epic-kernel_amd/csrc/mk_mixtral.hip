@@ -105,6 +105,11 @@ constexpr int kScratchSlotBase = 16;
 // folds the parts back into the barrier tensor.
 constexpr int kSpread = 8;
 constexpr int kSpreadAlign = 1024;
+// opcodes whose layer counters are spread, per kernel (bit k = opcode k):
+// provisional, set from measurements
+constexpr int32_t kSpreadDenseOps = (1 << 4) | (1 << 5) | (1 << 6);
+constexpr int32_t kSpreadMixtralOps = (1 << 4) | (1 << 5) | (1 << 6);
+constexpr int32_t kSpreadMoeOps = 0;
 constexpr int kPoolGroup = MK_POOL_GROUP;
 constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) that can be shared
 static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
@@ -199,6 +204,11 @@ struct KParams {
     // dynamic LDS); 0: off
     int32_t stage_items;
     int32_t stage_off16;
+    // nonzero: every instruction waits for its inputs before it issues any
+    // load, and nothing is staged for a later instruction (the prefetch-off
+    // side of an A/B; stage_items is then 0).  Whole-model and dense
+    // launches; the MoE-only kernel ignores it.
+    int32_t late_loads;
     int32_t lds_bytes;  // dynamic LDS of the launch
     // opcode-5/6 overlap (NULL: off): finished SiLU rows of both selected
     // experts per (layer, 512-row column chunk of F), counted by opcode 5 as
@@ -210,6 +220,7 @@ struct KParams {
     // (layer, opcode) rows, spread_stride ints apart
     int32_t *spread;
     int32_t spread_rows, spread_stride;
+    int32_t spread_ops;  // bit k: rows of opcode k are spread
     AttnParams attn_params;  // read only through attn_of()
 };
 
@@ -407,7 +418,8 @@ __device__ __forceinline__ int spread_row(const KParams &p, const int32_t *ctr) 
     const long off = ctr - p.bar;
     if (off < 0 || off % p.bar_width != 0) return -1;
     const long row = off / p.bar_width;
-    return row < p.spread_rows ? (int)row : -1;
+    if (row >= p.spread_rows || !((p.spread_ops >> (row % p.bar_ops + 1)) & 1)) return -1;
+    return (int)row;
 }
 
 // One lane adds n arrivals to counter `ctr`.  A few hundred workgroups that
@@ -971,6 +983,8 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
         sh.grp_done[0] = 0;
     }
     consumed = K;
+    auto wait = [&] { return wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer); };
+    if (kSpec && p.late_loads && !wait()) return false;  // whole-model launches only
     RouterRegs<kE> rr;
     router_prefetch<kE>(p, sh, layer, p.router, rr);
     // items 0 .. kWaves-1 go to waves 0 .. kWaves-1, the rest through the
@@ -979,54 +993,37 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     // the pool's instruction list does not depend on the producers either
     if (p.work_sharing) pool_scan(p, sh, layer, c.worker / kPoolGroup);
     const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
-    // Speculative early loads (whole-model launches, the reference's
-    // mx/rms_router_matvec.cu:259-290 re-expressed): once opcode 8 has
-    // predicted this layer's experts (checked, never waited for), waves 1 ..
-    // stage_items stream their first item of the predicted top-1 expert (a
-    // gate row and an up row) into LDS with global_load_lds while the
-    // workgroup waits for the O projection; if the routing then agrees, those
-    // items are computed from LDS.  A wrong prediction only costs the loads.
-    // Wave 0 stages nothing: thread 0 polls the counter, and a poll waits for
-    // every load its wave issued before it.  (Warming the same rows into L2
-    // instead gained nothing: 32 compute units x 128 KiB fill an XCD's 4 MiB
-    // L2, which the O projection streams through meanwhile.)
+    // Speculative early loads (whole-model launches): the preceding O
+    // projection may have staged this instruction's first items of the
+    // predicted top-1 expert in LDS (stage_moe_upgate).  Staging them here
+    // instead, at the start of opcode 5, gained nothing: 256 workgroups then
+    // load 28 MB at the moment the O projection hands over, which delays
+    // every workgroup's detection of that hand-off by ~4 us.
     int staged = 0;  // items 1 .. staged of this instruction are in LDS (of expert spec_e[0])
-    if constexpr (kSpec) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const bool predicted = !p.work_sharing && counter_reached(p, sh, bar_at(p, layer, 8), 1);
+    if constexpr (kSpec && kE > 0) {
         if (threadIdx.x == 0) {
-            int e0 = -1, e1 = -1;
-            if (predicted) {
-                e0 = (int)ld_dev32(p.pred_idx);
-                e1 = (int)ld_dev32(p.pred_idx + 1);
-                if (e0 < 0 || e0 >= p.E || e1 < 0 || e1 >= p.E) e0 = e1 = -1;
+            if (sh.stage_slot != c.slot) {
+                // the prediction only for the timing record
+                int e0 = -1, e1 = -1;
+                if (tim != nullptr && !p.work_sharing) {
+                    const int32_t *pc = bar_at(p, layer, 8);
+                    if (counter_value(p, pc, spread_row(p, pc)) >= 1) {
+                        e0 = (int)ld_dev32(p.pred_idx);
+                        e1 = (int)ld_dev32(p.pred_idx + 1);
+                    }
+                }
+                sh.spec_e[0] = e0;
+                sh.spec_e[1] = e1;
+            } else if (tim != nullptr) {
+                sh.spec_e[1] = (int)ld_dev32(p.pred_idx + 1);
             }
-            sh.spec_e[0] = e0;
-            sh.spec_e[1] = e1;
         }
         __syncthreads();
-        const int pe0 = __builtin_amdgcn_readfirstlane(sh.spec_e[0]);
-        // (only in the 8-expert kernel: the expert-count-generic one would spill)
-        if (kE > 0 && pe0 >= 0) {
-            staged = min(p.stage_items, nrows - 1);
-            stamp(tim, MK_TEVENT_FIRST_USE);
-            if (wave >= 1 && wave <= staged) {
-                const int nc = p.H / kChunkElems;
-                const size_t off = ((size_t)(layer * p.E + pe0) * p.F + row0 + wave) * (size_t)p.H;
-                const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
-                const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
-                u32x4 *dst = act + p.stage_off16 + (wave - 1) * 2 * nc * 64;
-                for (int i = 0; i < nc; ++i) {
-                    __builtin_amdgcn_global_load_lds((global_void_t *)(wg + i * 64), (lds_void_t *)(dst + i * 64),
-                                                     16, 0, 0);
-                    __builtin_amdgcn_global_load_lds((global_void_t *)(wu + i * 64),
-                                                     (lds_void_t *)(dst + (nc + i) * 64), 16, 0, 0);
-                }
-            }
-        }
+        staged = __builtin_amdgcn_readfirstlane(sh.stage_slot == c.slot ? sh.stage_n : 0);
+        if (staged > 0) stamp(tim, MK_TEVENT_FIRST_USE);
     }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
+    if (!(kSpec && p.late_loads) && !wait()) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
     float logits[Experts<kE>::kMax];
@@ -1380,7 +1377,7 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
     // Early loads: when this workgroup routed the layer itself (opcode 5 ran
     // here), the experts are known before the barrier, so each wave starts
     // streaming the first chunks of its first item while it waits.
-    const bool known = sh.route_layer == layer;
+    const bool known = !(!kOverlap && p.late_loads) && sh.route_layer == layer;  // late loads: whole-model only
     if (kOverlap && p.chunk_ctr != nullptr && known && nrows <= 32 && nrows % kItemRows == 0 && (p.F % kChunkElems) == 0 &&
         nc <= kGroupChunks * kMaxGroups)
         return downproj_overlapped(p, sh, act, c, tim, layer, start, end);
@@ -1510,9 +1507,11 @@ __device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u3
         return false;
     }
     const uint16_t *weights = p.predictor != nullptr ? p.predictor : p.router;
+    if (p.late_loads && layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 8, layer))
+        return false;
     RouterRegs<kE> rr;
     router_prefetch<kE>(p, sh, layer, weights, rr);
-    if (layer > 0) {
+    if (!p.late_loads && layer > 0) {
         stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
         if (!wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 8, layer)) return false;
         stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
@@ -1696,6 +1695,8 @@ __device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 
     if (threadIdx.x == 0) sh.next_item = kWaves;
     const int r0 = b0 * a.qkv_bs, nrows = (b1 - b0) * a.qkv_bs;
     const uint16_t *wq = a.qkv + (size_t)layer * qkv_rows * p.H;
+    auto wait = [&] { return layer == 0 || wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 1, layer); };
+    if (p.late_loads && !wait()) return false;
     PairAhead pre;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     const int nc = p.H / kChunkElems;
@@ -1706,7 +1707,7 @@ __device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 
     const int nst = min(max(nrows / 2 - kWaves, 0), max(p.lds_bytes / 16 - soff16, 0) / (2 * nc * 64));
     stage_pairs(wq, (size_t)p.H, 0, nc, r0, nst, act + soff16);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (layer > 0 && !wait_ge(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals, c, 1, layer)) return false;
+    if (!p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.attn_ln + (size_t)layer * p.H);
 
@@ -1857,15 +1858,15 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, Shared
                      dp);
         }
     };
-    stamp(tim, MK_TEVENT_FIRST_LOAD);
-    stage_chunks(0, nb);
-
     // producers: the GQA query heads, the key head and the value head
     const int bph = D / a.qkv_bs;
     const int32_t *bar_qkv = bar_at(p, layer, 1);
     const int32_t *mine = bar_qkv + (lane < GQA ? h0 + lane : lane == GQA ? a.Hq + kv : a.Hq + a.Hkv + kv);
+    if (p.late_loads && !wait_lanes_ge(p, sh, mine, GQA + 2, bph, c, 2, layer)) return false;
+    stamp(tim, MK_TEVENT_FIRST_LOAD);
+    stage_chunks(0, nb);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_lanes_ge(p, sh, mine, GQA + 2, bph, c, 2, layer)) return false;
+    if (!p.late_loads && !wait_lanes_ge(p, sh, mine, GQA + 2, bph, c, 2, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
     const float qscale = a.attn_scale * kLog2e;
@@ -2190,6 +2191,56 @@ __device__ __forceinline__ void stage_dense_upgate(const KParams &p, SharedState
     }
 }
 
+// Mixtral whole-model launches: the first items (a gate row and an up row
+// each) of the opcode-5 instruction `nx` that follows this O projection in
+// the queue (slot `slot`), of the expert opcode 8 predicted first, streamed
+// into LDS by waves 1 .. stage_items (one item each, item w = wave w's first
+// item there) with global_load_lds while the workgroup waits for the
+// attention reduction -- the reference's speculative expert prefetch
+// (mx/rms_router_matvec.cu:259-290), placed where HBM is idle: during
+// partial attention and the reduction.  Only when the prediction is in and
+// no reduction has arrived yet, so the loads land well before the wait
+// ends (the O projection's later loads queue behind them).  Opcode 5 uses
+// the rows if its routing picks the predicted expert first.  Wave 0 stages
+// nothing: its thread 0 polls the counter.
+__device__ __forceinline__ void stage_moe_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *nx, int slot,
+                                                 int layer) {
+    if (p.stage_items <= 0 || slot >= p.queue_len) return;
+    const int op = __builtin_amdgcn_readfirstlane(nx[0]);
+    const int l = __builtin_amdgcn_readfirstlane(nx[1]);
+    const int start = __builtin_amdgcn_readfirstlane(nx[2]);
+    const int nb = __builtin_amdgcn_readfirstlane(nx[3]);
+    if (op != 5 || l != layer || start < 0 || nb < 1 || (int64_t)(start + nb) * p.expert_bs > p.F) return;
+    if (threadIdx.x == 0) {
+        // prediction counter, reduction counter and the prediction, one round trip
+        const int32_t *pc = bar_at(p, layer, 8), *rc = bar_at(p, layer, 3);
+        const int pv = counter_value(p, pc, spread_row(p, pc)), rv = counter_value(p, rc, spread_row(p, rc));
+        const int e0 = (int)ld_dev32(p.pred_idx);
+        sh.spec_e[0] = pv >= 1 && rv == 0 && e0 >= 0 && e0 < p.E ? e0 : -1;
+    }
+    __syncthreads();
+    const int pe0 = __builtin_amdgcn_readfirstlane(sh.spec_e[0]);
+    if (pe0 < 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = start * p.expert_bs, S = min(p.stage_items, nb * p.expert_bs - 1);
+    if (wave >= 1 && wave <= S) {
+        const int nc = p.H / kChunkElems;
+        const size_t off = ((size_t)(layer * p.E + pe0) * p.F + row0 + wave) * (size_t)p.H;
+        const u32x4 *wg = reinterpret_cast<const u32x4 *>(p.gate + off) + lane;
+        const u32x4 *wu = reinterpret_cast<const u32x4 *>(p.up + off) + lane;
+        u32x4 *dst = act + p.stage_off16 + (wave - 1) * 2 * nc * 64;
+        for (int i = 0; i < nc; ++i) {
+            __builtin_amdgcn_global_load_lds((global_void_t *)(wg + i * 64), (lds_void_t *)(dst + i * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_t *)(wu + i * 64), (lds_void_t *)(dst + (nc + i) * 64), 16,
+                                             0, 0);
+        }
+    }
+    if (threadIdx.x == 0) {
+        sh.stage_slot = slot;
+        sh.stage_n = S;
+    }
+}
+
 __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                          int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
@@ -2210,7 +2261,9 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     // The residual rows of each wave's first item are final once the
     // previous layer's down-projection is complete (or at layer 0): read
     // them now instead of after the sums (one dependent load less).
-    const bool hfinal = (layer == 0 || counter_reached(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals)) &&
+    if (p.late_loads && !wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
+    const bool hfinal = !p.late_loads &&
+                        (layer == 0 || counter_reached(p, sh, bar_at(p, layer - 1, 6), p.down_arrivals)) &&
                         2 * wave < nrows;  // uniform
     const int rpre = r0 + 2 * wave;
     uint32_t hpair = 0;
@@ -2218,9 +2271,12 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     PairAhead pre;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, r0, nrows);
-    stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+    if (p.E == 1)
+        stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+    else
+        stage_moe_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
+    if (!p.late_loads && !wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(a.attn_out, (uint32_t)v * 16u);
     __syncthreads();
@@ -2314,10 +2370,11 @@ __device__ __forceinline__ bool lm_head_rows(const KParams &p, SharedState &sh, 
     constexpr int NR = LmRows<NC>::kNR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     u32x4 w[NR][NC];
+    if (p.late_loads && !wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     if (wave * NR < nrows) load_rows_upto<NR, NC>(w, a.lm_head, (size_t)p.H, r0 + wave * NR, min(NR, nrows - wave * NR), col0, lane);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
+    if (!p.late_loads && !wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.lm_norm);
     rows_matvec<NR, NC>(sh, w, a.lm_head, (size_t)p.H, col0, act + (col0 >> 3), r0, nrows,
@@ -2432,10 +2489,12 @@ __device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &s
                 }
         }
     };
+    auto wait = [&] { return wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer); };
+    if (p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     load_ahead();
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer)) return false;
+    if (!p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     if (threadIdx.x == 0) {
         sh.stage_slot = -1;  // every thread has read it (the wait ends in barriers)
@@ -2511,10 +2570,12 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
     const int r0 = b0 * p.down_bs, nitems = (b1 - b0) * p.down_bs / NR;
     const uint16_t *wm = p.down + (size_t)layer * p.H * p.F;
     u32x4 w[NR][NC];
+    auto wait = [&] { return wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer); };
+    if (p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     if (wave < nitems) load_rows<NR, NC>(w, wm, (size_t)p.F, r0 + wave * NR, col0, lane);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
+    if (!p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     for (int v = threadIdx.x; v < (R >> 3); v += kThreads) act[v] = ld_dev128(p.silu, (uint32_t)(col0 + v * 8) * 2u);
     __syncthreads();
@@ -2562,16 +2623,18 @@ __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &s
     const int nc = p.F / kChunkElems;
     const uint16_t *wm = p.down + (size_t)layer * p.H * p.F;
     const int nearly = min(nrows, kRowBatch);  // rows whose residual is read before the wait
+    auto wait = [&] { return wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer); };
+    if (p.late_loads && !wait()) return false;
     RowRegs<kSegChunks> pre;  // up to a whole first row per wave (16 KiB), as many loads as a later item
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     if (wave < nrows)
         load_row<kSegChunks>(pre, reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + wave) * p.F) + lane,
                              min(nc, kSegChunks));
-    const bool hfinal = __builtin_amdgcn_readfirstlane(sh.route_layer) == layer;
+    const bool hfinal = !p.late_loads && __builtin_amdgcn_readfirstlane(sh.route_layer) == layer;
     uint32_t hpre = 0;
     if (hfinal && tid < nearly) hpre = ld_dev16(p.hidden + r0 + tid);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, layer, 5), p.F / p.expert_bs, c, 6, layer)) return false;
+    if (!p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     uint32_t *hrow = reinterpret_cast<uint32_t *>(sh.part);  // the residual rows read early
     if (hfinal && tid < nearly) hrow[tid] = hpre;
@@ -2646,10 +2709,11 @@ __device__ __forceinline__ bool dense_lm_head_rows(const KParams &p, SharedState
     constexpr int NR = LmRows<NC>::kNR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     u32x4 w[NR][NC];
+    if (p.late_loads && !wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     if (wave * NR < nrows) load_rows_upto<NR, NC>(w, a.lm_head, (size_t)p.H, r0 + wave * NR, min(NR, nrows - wave * NR), 0, lane);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
-    if (!wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
+    if (!p.late_loads && !wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.lm_norm);
     rows_matvec<NR, NC>(sh, w, a.lm_head, (size_t)p.H, 0, act, r0, nrows, [&](int r, float sa, float sb) {
@@ -3087,18 +3151,31 @@ int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t l
 // goes to the barrier tensor itself).
 struct SpreadLayout {
     bool on;
+    int32_t ops;
     size_t offset, rows, stride, end;
 };
 
-SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops) {
+// `ops`: bit k set spreads the counters of opcode k (the default is the
+// caller's); MK_SPREAD=<bits> overrides it for measurements.
+SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops, int32_t ops) {
     SpreadLayout s{};
     const char *env = std::getenv("MK_SPREAD");
-    s.on = env == nullptr || env[0] != '0';
+    if (env != nullptr) ops = (int32_t)std::strtol(env, nullptr, 0);
+    s.ops = ops;
+    s.on = ops != 0;
     s.rows = (size_t)layers * (size_t)bar_ops;
     s.stride = (s.rows + kSpreadAlign - 1) / kSpreadAlign * kSpreadAlign;
     s.offset = (used + kSpreadAlign - 1) / kSpreadAlign * kSpreadAlign;
     s.end = s.on ? s.offset + (size_t)kSpread * s.stride : used;
     return s;
+}
+
+// Opcode-5 items staged ahead in LDS: `n` (what the LDS holds), none with
+// late loads; MK_STAGE_ITEMS=<k> caps it for measurements.
+size_t stage_limit(size_t n, bool late_loads) {
+    const char *env = std::getenv("MK_STAGE_ITEMS");
+    if (env != nullptr) n = std::min(n, (size_t)std::max(0L, std::strtol(env, nullptr, 0)));
+    return late_loads ? 0 : n;
 }
 
 uint32_t timeout_ticks(uint32_t spin_timeout_us) {
@@ -3299,11 +3376,11 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     const size_t stage_off = ((at0 * 2 + 1023) / 1024) * 1024;
     const size_t stage_item = (size_t)g->hidden_size * 4;
     const size_t lds_cap = (size_t)st->max_lds - sizeof(SharedState);
-    const size_t stage_items =
-        lds_cap > stage_off ? std::min((size_t)MK_STAGE_ITEMS, (lds_cap - stage_off) / stage_item) : 0;
+    const size_t stage_items = stage_limit(
+        lds_cap > stage_off ? std::min((size_t)MK_STAGE_ITEMS, (lds_cap - stage_off) / stage_item) : 0, g->late_loads);
     if (stage_items > 0) lds = std::max(lds, stage_off + stage_items * stage_item);
     const SpreadLayout sp = spread_layout(kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len,
-                                          g->num_layers, g->bar_ops);
+                                          g->num_layers, g->bar_ops, kSpreadDenseOps);
     rc = ensure_scratch(st, sp.end);
     if (rc != MK_OK) return rc;
 
@@ -3312,6 +3389,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.spread = sp.on ? st->scratch + sp.offset : nullptr;
     kp.spread_rows = (int32_t)sp.rows;
     kp.spread_stride = (int32_t)sp.stride;
+    kp.spread_ops = sp.ops;
     kp.scratch_clear = (int32_t)(2 * (size_t)g->num_workers * (size_t)g->queue_len);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
@@ -3339,6 +3417,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.scratch = st->scratch;
     kp.work_sharing = 0;
     kp.red_cols = g->matvec_reduction_size;
+    kp.late_loads = g->late_loads ? 1 : 0;
     kp.stage_items = (int32_t)stage_items;
     kp.stage_off16 = (int32_t)(stage_off / 16);
     kp.lds_bytes = (int32_t)lds;
@@ -3445,7 +3524,8 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const bool overlap = g->downproj_overlap != 0 && !g->work_sharing && g->num_experts == 8 &&
                          g->qkv_weights == nullptr;
     const size_t chunks = overlap ? (size_t)g->num_layers * (size_t)(g->intermediate_size / 512) : 0;
-    const SpreadLayout sp = spread_layout(kScratchSlotBase + cursors + chunks, g->num_layers, g->bar_ops);
+    const SpreadLayout sp = spread_layout(kScratchSlotBase + cursors + chunks, g->num_layers, g->bar_ops,
+                                          attn ? kSpreadMixtralOps : kSpreadMoeOps);
     rc = ensure_scratch(st, sp.end);
     if (rc != MK_OK) return rc;
 
@@ -3454,6 +3534,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.spread = sp.on ? st->scratch + sp.offset : nullptr;
     kp.spread_rows = (int32_t)sp.rows;
     kp.spread_stride = (int32_t)sp.stride;
+    kp.spread_ops = sp.ops;
     kp.scratch_clear = (int32_t)(cursors + chunks);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
@@ -3488,12 +3569,17 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
-    // whole-model launches: opcode 5 stages up to one predicted item per
-    // wave (but wave 0) in the LDS after the normed hidden state, within the
-    // launch's LDS (the opcode-2 ring makes it ~145 KiB at the Mixtral shape)
-    const size_t stage_off = (((size_t)g->hidden_size * 2 + 1023) / 1024) * 1024;
+    // whole-model launches: the O projection stages up to one predicted
+    // opcode-5 item per wave (but wave 0) in the LDS after its attention
+    // vector (opcode 5's normed hidden state), within the launch's LDS (the
+    // opcode-2 ring makes it ~145 KiB at the Mixtral shape)
+    const size_t at0 = attn ? std::max((size_t)g->hidden_size, (size_t)g->num_attention_heads * g->head_dim)
+                            : (size_t)g->hidden_size;
+    const size_t stage_off = ((at0 * 2 + 1023) / 1024) * 1024;
     const size_t stage_item = (size_t)g->hidden_size * 4;
-    kp.stage_items = attn && lds > stage_off ? (int32_t)std::min((size_t)(kWaves - 1), (lds - stage_off) / stage_item) : 0;
+    kp.late_loads = g->late_loads ? 1 : 0;
+    kp.stage_items = (int32_t)stage_limit(
+        attn && lds > stage_off ? std::min((size_t)(kWaves - 1), (lds - stage_off) / stage_item) : 0, g->late_loads);
     kp.stage_off16 = (int32_t)(stage_off / 16);
     kp.lds_bytes = (int32_t)lds;
     kp.argmax_out = g->argmax_out;

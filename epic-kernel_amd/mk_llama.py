@@ -13,8 +13,8 @@ under the reference's 3B module name.
 Keyword-only additions (defaults are the reference's compiled-in values):
 the block sizes and ``matvec_reduction_size`` the instructions were built
 with, ``spin_timeout_us``, ``record_timings``, ``argmax_out`` /
-``next_embed_weights``, ``reset_for_next_launch`` and ``debug_sync`` (as in
-``mk_mixtral``).  There is no fallback.
+``next_embed_weights``, ``reset_for_next_launch``, ``late_loads`` (prefetch
+off) and ``debug_sync`` (as in ``mk_mixtral``).  There is no fallback.
 """
 
 from __future__ import annotations
@@ -28,7 +28,7 @@ from mk_mixtral import MKError, _check, _check_tensor, _error_text, raise_if_fai
 
 __all__ = ["mk_llama", "mk_llama_3b", "MkLlamaGlobals", "build_llama_struct"]
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _P = ctypes.c_void_p
 
 
@@ -92,6 +92,7 @@ class MkLlamaGlobals(ctypes.Structure):
         ("argmax_out", ctypes.c_void_p),
         ("next_embed_weights", ctypes.c_void_p),
         ("reset_for_next_launch", ctypes.c_int32),
+        ("late_loads", ctypes.c_int32),
     ]
 
 
@@ -136,6 +137,7 @@ def build_llama_struct(
     argmax_out=None,
     next_embed_weights=None,
     reset_for_next_launch: bool = False,
+    late_loads: bool = False,
 ) -> MkLlamaGlobals:
     """Validate the reference-ordered arguments and fill the C struct;
     ``TypeError``/``ValueError`` before anything reaches the GPU."""
@@ -243,6 +245,7 @@ def build_llama_struct(
     g.record_timings = int(bool(record_timings))
     g.argmax_out, g.next_embed_weights = mk_mixtral._decode_tail(argmax_out, next_embed_weights, True, dev, H)
     g.reset_for_next_launch = int(bool(reset_for_next_launch))
+    g.late_loads = int(bool(late_loads))
     return g
 
 

@@ -40,6 +40,10 @@ sizes are the compile-time 16):
     the reference; ignored with ``work_sharing``); meant for an opcode-5
     partition interleaved across workers.  Same indices, scores and barrier
     counts; the hidden state differs only in fp32 summation order;
+``late_loads``
+    prefetch off: every instruction waits for its inputs before it loads
+    anything, and no predicted expert rows are staged (for prefetch on/off
+    comparisons; same results);
 ``debug_sync``
     synchronise after the launch and raise :class:`MKDeviceError` if the
     kernel recorded a failure.
@@ -69,7 +73,7 @@ __all__ = [
 _HERE = Path(__file__).resolve().parent
 _LIB_NAME = "libmk_mixtral.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 STATUS_WORDS = 16
 MAX_EXPERTS = 16
 
@@ -177,6 +181,7 @@ class MkMixtralGlobals(ctypes.Structure):
         ("next_embed_weights", _P),
         ("reset_for_next_launch", ctypes.c_int32),
         ("downproj_overlap", ctypes.c_int32),
+        ("late_loads", ctypes.c_int32),
     ]
 
 
@@ -331,6 +336,7 @@ def build_globals_struct(
     next_embed_weights=None,
     reset_for_next_launch: bool = False,
     downproj_overlap: bool = False,
+    late_loads: bool = False,
 ) -> MkMixtralGlobals:
     """Validate the reference-ordered arguments and fill the C struct.
 
@@ -445,6 +451,7 @@ def build_globals_struct(
     g.argmax_out, g.next_embed_weights = _decode_tail(argmax_out, next_embed_weights, attn is not None, dev, H)
     g.reset_for_next_launch = int(bool(reset_for_next_launch))
     g.downproj_overlap = int(bool(downproj_overlap))
+    g.late_loads = int(bool(late_loads))
     return g
 
 

@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define MK_LLAMA_ABI_VERSION 2
+#define MK_LLAMA_ABI_VERSION 3
 
 typedef struct mk_llama_globals {
     uint32_t struct_size;          /* sizeof(mk_llama_globals) */
@@ -125,6 +125,14 @@ typedef struct mk_llama_globals {
     const uint16_t *next_embed_weights; /* [V, H] bf16 or NULL: hidden_states := row *argmax_out */
     int32_t reset_for_next_launch;      /* nonzero: the barrier tensor is zeroed when the launch ends
                                            (the logits are stored, not accumulated, and need none) */
+
+    /* prefetch switch (no reference counterpart as a field: the reference
+     * sets its L2 lookahead at compile time, PREFETCH_LOOKAHEAD in
+     * demos/low-latency-llama/matvec_pipeline.cuh:19).  Nonzero: every
+     * instruction waits for its inputs before it issues any load, and no
+     * weights are staged in LDS for a later instruction; same results.
+     * For prefetch on/off comparisons. */
+    int32_t late_loads;
 } mk_llama_globals;
 
 /* Launch one decode step of the dense VM.  Returns MK_OK or an

@@ -69,7 +69,7 @@
 extern "C" {
 #endif
 
-#define MK_MIXTRAL_ABI_VERSION 4
+#define MK_MIXTRAL_ABI_VERSION 5
 #define MK_INTS_PER_INSTRUCTION 32
 #define MK_TIMING_SLOTS 128
 #define MK_STATUS_WORDS 16
@@ -238,6 +238,15 @@ typedef struct mk_mixtral_globals {
      * MoE-only launches (qkv_weights NULL) with 8 experts; ignored
      * otherwise. */
     int32_t downproj_overlap;
+
+    /* prefetch switch, no reference counterpart as a field (the reference
+     * always prefetches the predicted experts, demos/mixtral/
+     * rms_router_matvec.cu:259-290).  Nonzero: every instruction waits for
+     * its inputs before it issues any load (weights, KV rows, router rows),
+     * no predicted expert rows are staged, and opcode 6 takes no early
+     * loads; same results.  For prefetch on/off comparisons of whole-model
+     * launches (qkv_weights non-NULL); MoE-only launches ignore it. */
+    int32_t late_loads;
 } mk_mixtral_globals;
 
 /* Launch one persistent-kernel pass over the instruction queues.

@@ -12,7 +12,8 @@ the oracle in test_gpu_configs.py; here, what holds at any size:
   down-projection chunks, zero elsewhere;
 * a relaunch from the same input is bit-identical (token, logits, residual):
   with the default full-row down projection every residual row has one
-  writer, which adds in python_vm's order.
+  writer, which adds in python_vm's order; so is a launch with prefetch off
+  (``late_loads``: no load before its wait, nothing staged in LDS).
 """
 
 import pytest
@@ -36,7 +37,7 @@ def model():
     torch.cuda.empty_cache()
 
 
-def _launch(gen, token: int, pos: int):
+def _launch(gen, token: int, pos: int, **kw):
     import mk_llama
     from megakernels_amd.latency.mk import interpret_with_mk
 
@@ -46,7 +47,7 @@ def _launch(gen, token: int, pos: int):
     g.logits.zero_()
     g.pos_id = pos
     out = torch.full((), -1, dtype=torch.long, device="cuda")
-    interpret_with_mk(g, mk_llama.mk_llama, argmax_out=out, debug_sync=True)
+    interpret_with_mk(g, mk_llama.mk_llama, argmax_out=out, debug_sync=True, **kw)
     torch.cuda.synchronize()
     return out
 
@@ -80,3 +81,7 @@ def test_fullsize_dense_decode_properties(model):
     assert int(tok2) == int(tok)
     assert torch.equal(g.logits.cpu(), logits), "relaunch changed the logits"
     assert torch.equal(g.hidden_states.cpu(), hidden), "relaunch changed the residual"
+    tok3 = _launch(gen, 777, PREFILL, late_loads=True)
+    assert int(tok3) == int(tok)
+    assert torch.equal(g.logits.cpu(), logits), "prefetch off changed the logits"
+    assert torch.equal(g.hidden_states.cpu(), hidden), "prefetch off changed the residual"

@@ -13,7 +13,9 @@ same shapes are checked against the oracle in test_gpu_configs.py):
   F / expert_proj_block_size up/gate blocks, 2 H / down_proj_block_size
   down blocks and one prediction, and zero elsewhere;
 * a relaunch from the same input is bit-identical (token, logits, residual,
-  the appended K/V rows): the Mixtral path adds in a fixed order;
+  the appended K/V rows): the Mixtral path adds in a fixed order; so is a
+  launch with prefetch off (``late_loads``: no load before its wait, no
+  predicted expert rows staged in LDS), which reads the same values later;
 * the logits are finite and not all zero.
 
 Config 4 decodes at position 4096 and config 5 at 16384 (predictor weights =
@@ -42,7 +44,7 @@ def model():
     torch.cuda.empty_cache()
 
 
-def _launch(gen, token: int, pos: int):
+def _launch(gen, token: int, pos: int, **kw):
     import mk_mixtral
     from megakernels_amd.mixtral.mk import interpret_with_mk
 
@@ -52,7 +54,7 @@ def _launch(gen, token: int, pos: int):
     g.logits.zero_()
     g.pos_id = pos
     out = torch.full((), -1, dtype=torch.long, device="cuda")
-    interpret_with_mk(g, mk_mixtral.mk_mixtral, argmax_out=out, debug_sync=True)
+    interpret_with_mk(g, mk_mixtral.mk_mixtral, argmax_out=out, debug_sync=True, **kw)
     torch.cuda.synchronize()
     return out
 
@@ -94,5 +96,12 @@ def test_fullsize_decode_properties(model, pos):
              "pred": g.predicted_expert_indices.cpu()}
     for k in first:
         assert torch.equal(first[k], again[k]), f"relaunch changed {k}"
+    tok3 = _launch(gen, 1234, pos, late_loads=True)
+    assert int(tok3) == int(tok)
+    late = {"logits": g.logits.cpu(), "hidden": g.hidden_states.cpu(), "k": g.k_cache[:, 0, pos].cpu(),
+            "v": g.v_cache[:, 0, pos].cpu(), "sel": g.selected_expert_indices.cpu(),
+            "pred": g.predicted_expert_indices.cpu()}
+    for k in first:
+        assert torch.equal(first[k], late[k]), f"prefetch off changed {k}"
     print(f"[fullsize pos {pos}] token {int(tok)}, last layer experts {first['sel'].tolist()} "
           f"(predicted {first['pred'].tolist()})", flush=True)
