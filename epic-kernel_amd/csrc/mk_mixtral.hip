@@ -3008,6 +3008,21 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
 
 constexpr int kMaxDevices = 64;
 
+// Fixed scratch of mk_mixtral_launch_noalloc (2 MiB per device, held until
+// the process ends): ints [0, kNoAllocStatusInts) are its status words when
+// the caller passes none, the launch's scratch (exit counter, work-sharing
+// cursors, column-chunk counters, spread counters) starts at
+// kNoAllocBaseInts.  Every workgroup leaves through kernel_exit, whose last
+// workgroup zeroes what the launch used, so each launch finds it zero (as
+// the module loaded it).  Host code never passes `scratch` itself to a
+// kernel: its address on a device comes from hipGetSymbolAddress
+// (DeviceState::noalloc_scratch).
+constexpr size_t kNoAllocScratchInts = (size_t)1 << 19;
+constexpr size_t kNoAllocStatusInts = MK_STATUS_WORDS;
+constexpr size_t kNoAllocBaseInts = 64;  // 256-byte aligned
+static_assert(kNoAllocStatusInts <= kNoAllocBaseInts, "status words overlap the launch scratch");
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchInts];
+
 // Library state per device.  The scratch buffer (exit counter, work-sharing
 // cursors, column-chunk counters) and the status words are shared by every
 // launch on the device, and a persistent kernel needs all of its workgroups
@@ -3027,6 +3042,8 @@ struct DeviceState {
     bool launched = false;
     hipStream_t last_stream = nullptr;
     hipEvent_t order_event = nullptr;
+    // this device's copy of `scratch` (mk_mixtral_launch_noalloc), set once
+    int32_t *noalloc_scratch = nullptr;
 };
 
 std::mutex g_mutex;
@@ -3040,21 +3057,40 @@ int hip_fail(hipError_t e, const char *site) {
     return MK_ERR_HIP;
 }
 
-// `dev` must be the current device.
-int device_state(int dev, DeviceState **out) {
+// `dev` must be the current device.  The device attributes are read once;
+// the library-owned status words are allocated on the first call that asks
+// for them (`with_status`), the no-allocation launch's fixed scratch is
+// looked up on the first call that asks for it (`with_noalloc`).
+int device_state(int dev, DeviceState **out, bool with_status = true, bool with_noalloc = false) {
     if (dev < 0 || dev >= kMaxDevices) return MK_ERR_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lock(g_mutex);
     DeviceState &st = g_devices[dev];
+    hipError_t e;
     if (!st.ready) {
-        hipError_t e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+        e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
         e = hipDeviceGetAttribute(&st.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
         if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
-        e = hipMalloc(reinterpret_cast<void **>(&st.status), MK_STATUS_WORDS * sizeof(int32_t));
-        if (e != hipSuccess) return hip_fail(e, "hipMalloc");
-        e = hipMemset(st.status, 0, MK_STATUS_WORDS * sizeof(int32_t));
-        if (e != hipSuccess) return hip_fail(e, "hipMemset");
         st.ready = true;
+    }
+    if (with_status && st.status == nullptr) {
+        int32_t *s = nullptr;
+        e = hipMalloc(reinterpret_cast<void **>(&s), MK_STATUS_WORDS * sizeof(int32_t));
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+        e = hipMemset(s, 0, MK_STATUS_WORDS * sizeof(int32_t));
+        if (e != hipSuccess) {
+            (void)hipFree(s);
+            return hip_fail(e, "hipMemset");
+        }
+        st.status = s;
+    }
+    if (with_noalloc && st.noalloc_scratch == nullptr) {
+        // each device holds its own copy of the array, at its own address
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                              "hipGetSymbolAddress");
+        st.noalloc_scratch = static_cast<int32_t *>(ptr);
     }
     *out = &st;
     return MK_OK;
@@ -3107,8 +3143,12 @@ int ensure_scratch(DeviceState *st, size_t need) {
 // all the work queued there.  If that stream no longer exists (recording
 // fails), its work has been handed to the device already, and a device
 // synchronisation covers it.
-int order_after_previous(DeviceState *st, hipStream_t stream) {
+int order_after_previous(DeviceState *st, hipStream_t stream, bool may_allocate) {
     if (!st->launched || st->last_stream == stream) return MK_OK;
+    // the no-allocation launch records and waits on nothing (its callers may
+    // be capturing a graph, where a wait on another stream's event is not
+    // allowed): its caller orders it after launches on other streams
+    if (!may_allocate) return MK_OK;
     hipError_t e;
     if (st->order_event == nullptr &&
         (e = hipEventCreateWithFlags(&st->order_event, hipEventDisableTiming)) != hipSuccess)
@@ -3128,12 +3168,12 @@ int order_after_previous(DeviceState *st, hipStream_t stream) {
 // launch of `fn` (a persistent kernel over `workers` workgroups).  The
 // caller holds st->launch_mutex.
 int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t lds, KParams &kp,
-                      hipStream_t stream) {
+                      hipStream_t stream, bool may_allocate = true) {
     int blocks = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds);
     if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (workers > (int64_t)blocks * st->num_cus) return MK_ERR_NOT_CORESIDENT;
-    const int rc = order_after_previous(st, stream);
+    const int rc = order_after_previous(st, stream, may_allocate);
     if (rc != MK_OK) return rc;
     void *args[] = {&kp};
     e = hipLaunchKernel(fn, dim3((unsigned)workers), dim3(kThreads), args, lds, stream);
@@ -3473,6 +3513,9 @@ const char *mk_mixtral_error_string(int code) {
     case MK_ERR_UNSUPPORTED: return "shape or configuration not supported by the kernel";
     case MK_ERR_HIP: return "HIP runtime error";
     case MK_ERR_NOT_CORESIDENT: return "worker count exceeds co-resident workgroups";
+    case MK_ERR_SCRATCH_TOO_SMALL:
+        return "the launch needs more scratch than mk_mixtral_launch_noalloc's fixed 2 MiB array holds "
+               "(fewer workers x queue slots)";
     case MK_ERR_TIMEOUT: return "barrier wait timed out";
     case MK_ERR_BAD_OPCODE: return "unknown opcode";
     case MK_ERR_UNSUPPORTED_OPCODE: return "opcode not implemented by this kernel (attention / LM head)";
@@ -3496,14 +3539,17 @@ int mk_mixtral_query_device(int device, int32_t *num_cus, int32_t *max_workers) 
     return MK_OK;
 }
 
-int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
+// mk_mixtral_launch and mk_mixtral_launch_noalloc: `noalloc` takes the
+// launch's scratch from the fixed device array (and its status words there
+// too when the caller passes none) and allocates nothing.
+static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noalloc) {
     int rc = validate(g);
     if (rc != MK_OK) return rc;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     DeviceState *st = nullptr;
-    rc = device_state(dev, &st);
+    rc = device_state(dev, &st, !noalloc, noalloc);
     if (rc != MK_OK) return rc;
     std::lock_guard<std::mutex> launch_lock(st->launch_mutex);
 
@@ -3526,12 +3572,19 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     const size_t chunks = overlap ? (size_t)g->num_layers * (size_t)(g->intermediate_size / 512) : 0;
     const SpreadLayout sp = spread_layout(kScratchSlotBase + cursors + chunks, g->num_layers, g->bar_ops,
                                           attn ? kSpreadMixtralOps : kSpreadMoeOps);
-    rc = ensure_scratch(st, sp.end);
-    if (rc != MK_OK) return rc;
+    int32_t *base = nullptr;
+    if (noalloc) {
+        if (sp.end > kNoAllocScratchInts - kNoAllocBaseInts) return MK_ERR_SCRATCH_TOO_SMALL;
+        base = st->noalloc_scratch + kNoAllocBaseInts;
+    } else {
+        rc = ensure_scratch(st, sp.end);
+        if (rc != MK_OK) return rc;
+        base = st->scratch;
+    }
 
     KParams kp;
-    kp.chunk_ctr = overlap ? st->scratch + kScratchSlotBase + cursors : nullptr;
-    kp.spread = sp.on ? st->scratch + sp.offset : nullptr;
+    kp.chunk_ctr = overlap ? base + kScratchSlotBase + cursors : nullptr;
+    kp.spread = sp.on ? base + sp.offset : nullptr;
     kp.spread_rows = (int32_t)sp.rows;
     kp.spread_stride = (int32_t)sp.stride;
     kp.spread_ops = sp.ops;
@@ -3539,7 +3592,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
     kp.bar = g->barriers;
-    kp.status = g->status != nullptr ? g->status : st->status;
+    kp.status = g->status != nullptr ? g->status : noalloc ? st->noalloc_scratch : st->status;
     kp.gate = g->expert_gate_weights;
     kp.up = g->expert_up_weights;
     kp.down = g->expert_down_weights;
@@ -3565,7 +3618,7 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     kp.oproj_bs = g->o_proj_block_size;
     kp.eps = g->rms_norm_eps;
     kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
-    kp.scratch = st->scratch;
+    kp.scratch = base;
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
@@ -3620,8 +3673,12 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) {
     }
     kp.pos = g->pos_id;
     // fn is one of the four instantiations above
-    return launch_persistent(fn, st, g->num_workers, lds, kp, reinterpret_cast<hipStream_t>(stream));
+    return launch_persistent(fn, st, g->num_workers, lds, kp, reinterpret_cast<hipStream_t>(stream), !noalloc);
 }
+
+int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream) { return launch_mixtral(g, stream, false); }
+
+int mk_mixtral_launch_noalloc(const mk_mixtral_globals *g, void *stream) { return launch_mixtral(g, stream, true); }
 
 int mk_mixtral_read_status(int device, int32_t *out) {
     if (out == nullptr) return MK_ERR_INVALID_ARGUMENT;
@@ -3632,6 +3689,9 @@ int mk_mixtral_read_status(int device, int32_t *out) {
     if (rc != MK_OK) return rc;
     hipError_t e = hipDeviceSynchronize();
     if (e == hipSuccess) e = hipMemcpy(out, st->status, MK_STATUS_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost);
+    // no failure there: the status words of mk_mixtral_launch_noalloc
+    if (e == hipSuccess && out[MK_STATUS_CODE] == MK_OK && st->noalloc_scratch != nullptr)
+        e = hipMemcpy(out, st->noalloc_scratch, MK_STATUS_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
     return MK_OK;
 }
@@ -3644,6 +3704,8 @@ int mk_mixtral_clear_status(int device) {
     if (rc != MK_OK) return rc;
     hipError_t e = hipDeviceSynchronize();
     if (e == hipSuccess) e = hipMemset(st->status, 0, MK_STATUS_WORDS * sizeof(int32_t));
+    if (e == hipSuccess && st->noalloc_scratch != nullptr)
+        e = hipMemset(st->noalloc_scratch, 0, MK_STATUS_WORDS * sizeof(int32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
     return MK_OK;

@@ -83,6 +83,7 @@ _ERROR_NAMES = {
     2: "MK_ERR_UNSUPPORTED",
     3: "MK_ERR_HIP",
     4: "MK_ERR_NOT_CORESIDENT",
+    5: "MK_ERR_SCRATCH_TOO_SMALL",
     16: "MK_ERR_TIMEOUT",
     17: "MK_ERR_BAD_OPCODE",
     18: "MK_ERR_UNSUPPORTED_OPCODE",
@@ -188,6 +189,7 @@ class MkMixtralGlobals(ctypes.Structure):
 #: C entry points declared in include/mk_mixtral.h
 EXPORTED_SYMBOLS = (
     "mk_mixtral_launch",
+    "mk_mixtral_launch_noalloc",
     "mk_mixtral_read_status",
     "mk_mixtral_clear_status",
     "mk_mixtral_query_device",
@@ -216,6 +218,8 @@ def load_library():
     lib = ctypes.CDLL(str(path))
     lib.mk_mixtral_launch.argtypes = [ctypes.POINTER(MkMixtralGlobals), ctypes.c_void_p]
     lib.mk_mixtral_launch.restype = ctypes.c_int
+    lib.mk_mixtral_launch_noalloc.argtypes = [ctypes.POINTER(MkMixtralGlobals), ctypes.c_void_p]
+    lib.mk_mixtral_launch_noalloc.restype = ctypes.c_int
     lib.mk_mixtral_read_status.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int32)]
     lib.mk_mixtral_read_status.restype = ctypes.c_int
     lib.mk_mixtral_clear_status.argtypes = [ctypes.c_int]

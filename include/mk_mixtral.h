@@ -81,6 +81,8 @@ typedef enum mk_status_code {
     MK_ERR_UNSUPPORTED = 2,       /* shape outside what the kernel implements */
     MK_ERR_HIP = 3,               /* HIP runtime error, see mk_mixtral_last_hip_error */
     MK_ERR_NOT_CORESIDENT = 4,    /* grid cannot be fully resident            */
+    MK_ERR_SCRATCH_TOO_SMALL = 5, /* mk_mixtral_launch_noalloc: the launch needs
+                                     more than its fixed scratch holds       */
     MK_ERR_TIMEOUT = 16,          /* device: barrier spin timed out           */
     MK_ERR_BAD_OPCODE = 17,       /* device: opcode not in 0..8               */
     MK_ERR_UNSUPPORTED_OPCODE = 18, /* device: opcode 1-4 or 7                */
@@ -252,6 +254,26 @@ typedef struct mk_mixtral_globals {
 /* Launch one persistent-kernel pass over the instruction queues.
  * Replaces the pybind11 `mk_mixtral` (demos/mixtral/mixtral.cu:28-94). */
 int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream);
+
+/* Launch like mk_mixtral_launch, allocating nothing: no hipMalloc, hipFree,
+ * event or other allocating call, on any call (the first on a device
+ * included).  No counterpart in the reference: for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation.  The caller still passes every input and output.
+ *   - The launch's scratch (exit counter, two ints of work-sharing cursors
+ *     per instruction slot, column-chunk counters, spread layer counters)
+ *     lives in a fixed 2 MiB device array per device, held until the process
+ *     ends.  A launch that needs more -- about 2 x num_workers x queue_len
+ *     + 8 x 1024 ints -- returns MK_ERR_SCRATCH_TOO_SMALL without launching
+ *     (up to about 250000 instruction slots, e.g. 256 workers x 980).
+ *   - With `status` NULL, the status words are 16 ints of that array;
+ *     mk_mixtral_read_status / mk_mixtral_clear_status cover them.
+ *   - Every call on a device shares the array, and each launch leaves it
+ *     zeroed when its last workgroup exits.  Calls that overlap on one GPU
+ *     race: unlike mk_mixtral_launch, this entry point records and waits on
+ *     no event, so the caller orders it after launches on other streams
+ *     (one stream for all launches does that). */
+int mk_mixtral_launch_noalloc(const mk_mixtral_globals *g, void *stream);
 
 /* Copy the library-owned status words of `device` into out[16] after a
  * device-wide synchronisation.  No reference counterpart (the reference has
