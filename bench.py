@@ -306,7 +306,8 @@ def decode_bench(args, config: str, steps: int, warmup: int):
     gen = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                              dag_kwargs=None if llama else {"predict": not args.no_predict},
                              device_argmax=not args.host_argmax, reset_next=not args.no_reset,
-                             late_loads=args.late_loads)
+                             late_loads=args.late_loads, xcd_rows=tuple(int(x) for x in args.xcd_rows.split(",") if x),
+                             **({} if llama else {"work_sharing": not args.no_work_sharing}))
     print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
           f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
@@ -370,6 +371,7 @@ def decode_bench(args, config: str, steps: int, warmup: int):
             "partition_policy": args.partitions,
             "argmax": "torch, between launches" if args.host_argmax else "in-kernel, with the next embedding",
             "late_loads": args.late_loads,
+            "work_sharing": None if llama else not args.no_work_sharing,
             "fills_between_launches": args.host_argmax or args.no_reset,
         },
         "ms_per_step_hip_events": kernel_s * 1e3,
@@ -413,6 +415,8 @@ def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: di
     from megakernels_amd.mixtral.generate import MK_Generator
 
     base = {"device_argmax": not args.host_argmax, "reset_next": not args.no_reset}
+    if not llama:
+        base["work_sharing"] = not args.no_work_sharing
     variants = {"on": gen}
     variants["late_loads"] = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                                                 dag_kwargs=None if llama else {"predict": not args.no_predict},
@@ -676,6 +680,9 @@ def main():
     ap.add_argument("--no-reset", action="store_true",
                     help="c3/c4/c5: fill the barriers and logits before every launch instead of having each "
                          "launch zero them for the next")
+    ap.add_argument("--xcd-rows", default="", metavar="OPCODES",
+                    help="c3/c4/c5: comma-separated opcodes whose row ranges are regrouped so each XCD's workers "
+                         "take one contiguous span (group_rows_by_xcd)")
     ap.add_argument("--no-skewed", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
@@ -692,7 +699,9 @@ def main():
     ap.add_argument("--balance", action="store_true",
                     help="re-split rows by per-worker speed measured on a few launches (block size 1)")
     ap.add_argument("--work-sharing", action="store_true",
-                    help="idle workers take unclaimed opcode-5 rows of other workers")
+                    help="c1/c2: idle workers take unclaimed opcode-5 rows of other workers (c4/c5: the default)")
+    ap.add_argument("--no-work-sharing", action="store_true",
+                    help="c4/c5: every worker does exactly its own opcode-5 rows")
     ap.add_argument("--trace", default="", metavar="NPZ",
                     help="after the timed run, record the kernel's timing slots (8 launches for c1/c2, one decode "
                          "step for c3/c4/c5), save the last as NPZ and print the trace analysis to stderr")

@@ -64,6 +64,10 @@
 #ifndef MK_POOL_GROUP
 #define MK_POOL_GROUP 8
 #endif
+// O-projection rows staged in LDS by a preceding reduction (stage_oproj_rows).
+#ifndef MK_OSTAGE
+#define MK_OSTAGE 1
+#endif
 // Spin back-off: a waiting workgroup polls its counter every ~64 * N clocks,
 // N growing from 1 to MK_SPIN_SLEEP_MAX, so hundreds of idle workgroups do not
 // keep the counter's memory channel busy while others still stream weights.
@@ -104,6 +108,7 @@ constexpr int kScratchSlotBase = 16;
 // row-0 counter and its kSpread parts, and the last workgroup of the launch
 // folds the parts back into the barrier tensor.
 constexpr int kSpread = 8;
+constexpr int kXcds = 8;  // MI355X: workgroup w runs on XCD w % 8 (round-robin dispatch)
 constexpr int kSpreadAlign = 1024;
 // opcodes whose layer counters are spread, per kernel (bit k = opcode k):
 // provisional, set from measurements
@@ -112,6 +117,7 @@ constexpr int32_t kSpreadMixtralOps = (1 << 4) | (1 << 5) | (1 << 6);
 constexpr int32_t kSpreadMoeOps = 0;
 constexpr int kPoolGroup = MK_POOL_GROUP;
 constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) that can be shared
+constexpr int kPoolWindow = 8;  // queue slots per group member pool_scan_near looks at
 static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
 constexpr int kRowBatchLds = 64;  // rows per opcode-6 batch (partial sums in LDS)
 constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 16 * 512)
@@ -253,6 +259,9 @@ struct SharedState {
     // dense VM: queue slot whose first stage_n opcode-5 items opcode 4 staged
     // in LDS (-1: none)
     int stage_slot, stage_n;
+    // queue slot of the opcode 4 whose weight rows opcode 3 staged in LDS
+    // (-1: none)
+    int ostage_slot;
     // opcode 5 over consecutive instructions of one layer (kMaxMerge at
     // most): first FFN row, rows, first pooled item, finished items
     int grp_row0[kMaxMerge], grp_nrows[kMaxMerge], grp_first[kMaxMerge + 1], grp_done[kMaxMerge];
@@ -770,6 +779,23 @@ __device__ __forceinline__ void upgate_item(const KParams &p, const u32x4 *act, 
     silu_store(p, e, r, wave_sum(ag), wave_sum(au), lane);
 }
 
+// Item `it` of an opcode-5 instruction when its gate and up rows are the
+// ones this wave staged in LDS (the predicted top-1 expert's row row0 + it,
+// staged by the preceding O projection; the loads have landed once the wave
+// has waited for its own loads).
+__device__ __forceinline__ void upgate_item_staged(const KParams &p, const u32x4 *act, int row0, int e, int it,
+                                                   int wave, int lane) {
+    const int nc = p.H / kChunkElems;
+    const u32x4 *sg = act + p.stage_off16 + (wave - 1) * 2 * nc * 64 + lane, *su = sg + nc * 64;
+    __builtin_amdgcn_s_waitcnt(0);
+    float ag = 0.f, au = 0.f;
+    for (int ch = 0; ch < nc; ++ch) {
+        ag = dot8(sg[ch * 64], act[ch * 64 + lane], ag);
+        au = dot8(su[ch * 64], act[ch * 64 + lane], au);
+    }
+    silu_store(p, e, row0 + it, wave_sum(ag), wave_sum(au), lane);
+}
+
 // Wave-level claim of the next item of an instruction.  Lane 0 issues the
 // atomic; the value is broadcast only where it is needed, so the wait for the
 // atomic's return can sit behind the current item's weight loads.
@@ -779,50 +805,35 @@ __device__ __forceinline__ int claim_issue(int32_t *cursor, int lane) {
     return v;
 }
 
-// Collect the group's opcode-5 instructions of `layer` (all queue slots of
-// workers [group * kPoolGroup, +kPoolGroup)) into sh.pool_*, in (worker,
-// slot) order, so every member enumerates the pooled items identically.
-// Instructions with out-of-range operands are left out (their owner reports
-// them).  Ends with a workgroup barrier.
-__device__ __forceinline__ void pool_scan(const KParams &p, SharedState &sh, int layer, int group) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int w0 = group * kPoolGroup;
-    const int w1 = min((int)gridDim.x, w0 + kPoolGroup);
-    const int n = (w1 - w0) * p.queue_len;
-    if (tid == 0) sh.pool_n = 0;
-    __syncthreads();
-    for (int base = 0; base < n; base += kThreads) {
-        const int i = base + tid;
-        bool m = false;
-        int start = 0, nb = 0;
-        if (i < n) {
-            const int32_t *ins = p.instructions + ((size_t)w0 * p.queue_len + i) * MK_INTS_PER_INSTRUCTION;
-            start = ins[2];
-            nb = ins[3];
-            m = ins[0] == 5 && ins[1] == layer && start >= 0 && nb > 0 &&
-                (int64_t)(start + nb) * p.expert_bs <= (int64_t)p.F;
-        }
-        const uint64_t bal = __ballot(m);
-        if (lane == 0) sh.wave_cnt[wave] = __popcll(bal);
-        __syncthreads();
-        int off = sh.pool_n;
-        for (int v = 0; v < wave; ++v) off += sh.wave_cnt[v];
-        if (m) {
-            const int k = off + __popcll(bal & ((1ull << lane) - 1ull));
-            if (k < kMaxPoolIns) {
-                sh.pool_slot[k] = w0 * p.queue_len + i;
-                sh.pool_row0[k] = start * p.expert_bs;
-                sh.pool_nrows[k] = nb * p.expert_bs;
-            }
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int tot = 0;
-            for (int v = 0; v < kWaves; ++v) tot += sh.wave_cnt[v];
-            sh.pool_n += tot;
-        }
-        __syncthreads();
+// Wave 0 collects the group's opcode-5 instructions of `layer` (workers
+// [group * kPoolGroup, +kPoolGroup)) into sh.pool_*, in (worker, slot)
+// order, looking at the queue slots [slot - kPoolWindow / 2, +kPoolWindow)
+// of each member: the instructions of one layer sit at about the same queue
+// depth on every worker, and this way one round trip reads all of them
+// (wave 0 has no staging loads in flight ahead of it).  An instruction
+// outside the window is only left out of the sharing (its owner still does
+// all of its items); out-of-range operands are left out too (their owner
+// reports them).  The caller's next workgroup barrier publishes the pool.
+__device__ __forceinline__ void pool_scan_near(const KParams &p, SharedState &sh, int layer, int group, int slot) {
+    static_assert(kPoolGroup * kPoolWindow == 64, "pool_scan_near: one slot per lane of wave 0");
+    const int lane = threadIdx.x & 63;
+    const int w0 = group * kPoolGroup, mate = lane / kPoolWindow;
+    const int q = max(0, slot - kPoolWindow / 2) + lane % kPoolWindow;
+    int4 wd = make_int4(0, 0, 0, 0);
+    if (w0 + mate < (int)gridDim.x && q < p.queue_len)
+        wd = *reinterpret_cast<const int4 *>(p.instructions +
+                                             ((size_t)(w0 + mate) * p.queue_len + q) * MK_INTS_PER_INSTRUCTION);
+    const int start = wd.z, nb = wd.w;
+    const bool m = wd.x == 5 && wd.y == layer && start >= 0 && nb > 0 &&
+                   (int64_t)(start + nb) * p.expert_bs <= (int64_t)p.F;
+    const uint64_t bal = __ballot(m);
+    if (m) {
+        const int k = __popcll(bal & ((1ull << lane) - 1ull));
+        sh.pool_slot[k] = (w0 + mate) * p.queue_len + q;
+        sh.pool_row0[k] = start * p.expert_bs;
+        sh.pool_nrows[k] = nb * p.expert_bs;
     }
+    if (lane == 0) sh.pool_n = __popcll(bal);
 }
 
 __device__ __forceinline__ int tail_items(int items) { return items < MK_TAIL_ITEMS ? items : MK_TAIL_ITEMS; }
@@ -985,13 +996,15 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
     consumed = K;
     auto wait = [&] { return wait_ge(p, sh, bar_at(p, layer, 4), p.H / p.oproj_bs, c, 5, layer); };
     if (kSpec && p.late_loads && !wait()) return false;  // whole-model launches only
+    // the pool's instruction list does not depend on the producers either
+    // (the wait below, or rms_router's, is the workgroup barrier after it)
+    if (p.work_sharing && __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0)
+        pool_scan_near(p, sh, layer, c.worker / kPoolGroup, c.slot);
     RouterRegs<kE> rr;
     router_prefetch<kE>(p, sh, layer, p.router, rr);
     // items 0 .. kWaves-1 go to waves 0 .. kWaves-1, the rest through the
     // LDS counter (reset here; the wait below is a workgroup barrier)
     if (threadIdx.x == 0) sh.next_item = kWaves;
-    // the pool's instruction list does not depend on the producers either
-    if (p.work_sharing) pool_scan(p, sh, layer, c.worker / kPoolGroup);
     const int row0 = start * p.expert_bs, nrows = nb * p.expert_bs;
     // Speculative early loads (whole-model launches): the preceding O
     // projection may have staged this instruction's first items of the
@@ -1073,9 +1086,16 @@ __device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedSta
         while (self_k < sh.pool_n - 1 && sh.pool_slot[self_k] != self_slot) ++self_k;
         int32_t *cursor = slot_cursor(p, self_slot);
         const int items = 2 * nrows, tail = tail_items(items);
+        // a wave's first item (item `wave`) may be staged in LDS, as in the
+        // static path below
+        const bool from_lds = kSpec && kE > 0 && staged > 0 && wave >= 1 && wave <= staged && wave < nrows &&
+                              __builtin_amdgcn_readfirstlane(sh.spec_e[0]) == t.i0;
         int mine = 0;
         for (int it = wave; it < items - tail; it = next_local_item(sh, lane)) {
-            upgate_item(p, act, layer, row0, nrows, t.i0, t.i1, it, lane);
+            if (kSpec && kE > 0 && mine == 0 && from_lds)
+                upgate_item_staged(p, act, row0, t.i0, it, wave, lane);
+            else
+                upgate_item(p, act, layer, row0, nrows, t.i0, t.i1, it, lane);
             ++mine;
         }
         mine += upgate_claimed(p, act, layer, row0, nrows, t.i0, t.i1, items - tail, tail, cursor, lane);
@@ -1630,25 +1650,41 @@ __device__ __forceinline__ void stage_pairs(const uint16_t *mat, size_t ld, int 
 }
 
 // matvec_rows whose first item per wave was loaded by pair_ahead_load with
-// the same arguments, and whose pairs kWaves .. kWaves + nst - 1 were staged
-// at `stage` by stage_pairs.
+// the same arguments, except the row pairs sbase .. sbase + nst - 1, which
+// were staged at `stage` (row-major 512-column chunks in lane order) by
+// stage_pairs (sbase = kWaves) or stage_oproj_rows (sbase = 0: every pair,
+// nothing loaded ahead).  The summation order is the same in all three
+// forms.  fn(row, sum) per row, called by lane 0.
 template <typename Fn>
 __device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhead &pre, const uint16_t *mat,
                                                   size_t ld, int col0, int nc, const u32x4 *x, int r0, int nrows,
-                                                  Fn fn, const u32x4 *stage = nullptr, int nst = 0) {
+                                                  Fn fn, const u32x4 *stage = nullptr, int nst = 0,
+                                                  int sbase = kWaves) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    auto staged_pair = [&](int q, float &aa, float &ab) {
+        const u32x4 *sa = stage + (2 * q) * nc * 64 + lane, *sb = sa + nc * 64;
+        for (int ch = 0; ch < nc; ++ch) {
+            aa = dot8(sa[ch * 64], x[lane + ch * 64], aa);
+            ab = dot8(sb[ch * 64], x[lane + ch * 64], ab);
+        }
+    };
     if (2 * wave < nrows) {
         const int ra = r0 + 2 * wave;
         float aa = 0.f, ab = 0.f;
+        if (sbase == 0 && wave < nst) {
+            staged_pair(wave, aa, ab);
+        } else {
 #pragma unroll
-        for (int i = 0; i < kAheadChunks; ++i)
-            if (i < nc) {
-                aa = dot8(pre.a[i], x[lane + i * 64], aa);
-                ab = dot8(pre.b[i], x[lane + i * 64], ab);
+            for (int i = 0; i < kAheadChunks; ++i)
+                if (i < nc) {
+                    aa = dot8(pre.a[i], x[lane + i * 64], aa);
+                    ab = dot8(pre.b[i], x[lane + i * 64], ab);
+                }
+            if (nc > kAheadChunks) {
+                const uint16_t *row_a = mat + (size_t)ra * ld + col0 + kAheadChunks * kChunkElems;
+                dot_pair(row_a, row_a + ld, x + kAheadChunks * 64, x + kAheadChunks * 64, nc - kAheadChunks, lane,
+                         aa, ab);
             }
-        if (nc > kAheadChunks) {
-            const uint16_t *row_a = mat + (size_t)ra * ld + col0 + kAheadChunks * kChunkElems;
-            dot_pair(row_a, row_a + ld, x + kAheadChunks * 64, x + kAheadChunks * 64, nc - kAheadChunks, lane, aa, ab);
         }
         aa = wave_sum(aa);
         ab = wave_sum(ab);
@@ -1660,15 +1696,10 @@ __device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhe
     for (int it = next_local_item(sh, lane); 2 * it < nrows; it = next_local_item(sh, lane)) {
         const int ra = r0 + 2 * it;
         float aa = 0.f, ab = 0.f;
-        if (it - kWaves < nst) {
-            const u32x4 *sa = stage + (2 * (it - kWaves)) * nc * 64 + lane, *sb = sa + nc * 64;
-            for (int ch = 0; ch < nc; ++ch) {
-                aa = dot8(sa[ch * 64], x[lane + ch * 64], aa);
-                ab = dot8(sb[ch * 64], x[lane + ch * 64], ab);
-            }
-        } else {
+        if (it - sbase < nst)
+            staged_pair(it - sbase, aa, ab);
+        else
             dot_pair(mat + (size_t)ra * ld + col0, mat + (size_t)(ra + 1) * ld + col0, x, x, nc, lane, aa, ab);
-        }
         aa = wave_sum(aa);
         ab = wave_sum(ab);
         if (lane == 0) {
@@ -2073,7 +2104,37 @@ __device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &s
 
 // ---- opcode 3: Mixtral_AttnReduction  (python_vm.py:166-189) --------------
 
-__device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState &sh, ins_t *ins, const Ctx &c,
+// The worker's next instruction `nx` (queue slot `slot`), when it is the
+// O projection of `layer`: its weight rows depend on nothing, so opcode 3
+// streams them into LDS (row-major 512-column chunks in lane order, at the
+// staging offset) with global_load_lds while it waits for the partials,
+// on waves 1.. (wave 0 polls).  A reduction worker otherwise starts its O
+// projection's loads only when the reduction is done, and every other
+// workgroup's opcode 5 then waits for it.
+__device__ __forceinline__ void stage_oproj_rows(const KParams &p, const attn_c &a, SharedState &sh, u32x4 *act,
+                                                 ins_t *nx, int slot, int layer) {
+    if (p.late_loads || slot >= p.queue_len) return;
+    const int op = __builtin_amdgcn_readfirstlane(nx[0]);
+    const int l = __builtin_amdgcn_readfirstlane(nx[1]);
+    const int b0 = __builtin_amdgcn_readfirstlane(nx[2]);
+    const int b1 = __builtin_amdgcn_readfirstlane(nx[3]);
+    const int red = __builtin_amdgcn_readfirstlane(nx[4]);
+    if (op != 4 || l != layer || b0 < 0 || b1 <= b0 || (int64_t)b1 * p.oproj_bs > p.H || red != 0) return;
+    const int K = a.Hq * a.D, nc = K / kChunkElems, nrows = (b1 - b0) * p.oproj_bs;
+    if ((int64_t)p.stage_off16 * 16 + (int64_t)nrows * K * 2 > (int64_t)p.lds_bytes) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wave >= 1) {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(a.oproj + ((size_t)layer * p.H + (size_t)b0 * p.oproj_bs) * K) +
+                           (threadIdx.x & 63);
+        u32x4 *dst = act + p.stage_off16;
+        const int n = nrows * nc;
+        for (int pc = wave - 1; pc < n; pc += kWaves - 1)
+            __builtin_amdgcn_global_load_lds((global_void_t *)(src + pc * 64), (lds_void_t *)(dst + pc * 64), 16, 0, 0);
+    }
+    if (threadIdx.x == 0) sh.ostage_slot = slot;
+}
+
+__device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                                   int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int hs = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2094,6 +2155,7 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 3, layer, hs, n);
         return false;
     }
+    if (MK_OSTAGE) stage_oproj_rows(p, a, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 2) + hs, nparts, c, 3, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
@@ -2270,24 +2332,33 @@ __device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x
     if (hfinal && lane == 0) hpair = ld_dev32(p.hidden + rpre);
     PairAhead pre;
     stamp(tim, MK_TEVENT_FIRST_LOAD);
-    pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, r0, nrows);
-    if (p.E == 1)
-        stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
-    else
-        stage_moe_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+    // rows staged in LDS by the preceding opcode 3 (stage_oproj_rows; its
+    // loads were waited for before its last workgroup barrier): nothing to
+    // load, and the staging area is taken
+    const bool ostaged = MK_OSTAGE && __builtin_amdgcn_readfirstlane(sh.ostage_slot) == c.slot;
+    if (!ostaged) {
+        pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, r0, nrows);
+        if (p.E == 1)
+            stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+        else
+            stage_moe_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+    }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!p.late_loads && !wait_ge(p, sh, bar_at(p, layer, 3), a.Hq, c, 4, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     for (int v = threadIdx.x; v < (K >> 3); v += kThreads) act[v] = ld_dev128(a.attn_out, (uint32_t)v * 16u);
     __syncthreads();
-    matvec_rows_ahead(sh, pre, wo, (size_t)K, 0, K / kChunkElems, act, r0, nrows, [&](int r, float s) {
+    auto add_row = [&](int r, float s) {
         uint16_t *hp = p.hidden + r;
         const uint32_t h = hfinal && r == rpre       ? (hpair & 0xffffu)
                            : hfinal && r == rpre + 1 ? (hpair >> 16)
                                                      : ld_dev16(hp);
         st_dev16(hp, f2bf(bf2f(h) + rbf(s)));
-    });
+    };
+    matvec_rows_ahead(sh, pre, wo, (size_t)K, 0, K / kChunkElems, act, r0, nrows, add_row, act + p.stage_off16,
+                      ostaged ? nrows / 2 : 0, 0);
     drain_and_sync();
+    if (ostaged && threadIdx.x == 0) sh.ostage_slot = -1;  // every thread has read it
     arrive(p, bar_at(p, layer, 4), b1 - b0);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
@@ -2912,6 +2983,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
     if (threadIdx.x == 0) {
         sh.route_layer = -1;
         sh.stage_slot = -1;
+        sh.ostage_slot = -1;
     }
     __syncthreads();
 
@@ -2942,7 +3014,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
             if constexpr (kAttn) {
                 if (op == 1) ok = op_qkv(p, sh, act, ins, c, tim);
                 else if (op == 2) ok = op_partial_attn(p, sh, act, ins, c, tim);
-                else if (op == 3) ok = op_attn_reduction(p, sh, ins, c, tim);
+                else if (op == 3) ok = op_attn_reduction(p, sh, act, ins, c, tim);
                 else if (op == 4) ok = op_oproj(p, sh, act, ins, c, tim);
                 else ok = op_lm_head(p, sh, act, ins, c, tim);
             } else {
@@ -2970,6 +3042,7 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
     if (threadIdx.x == 0) {
         sh.route_layer = -1;
         sh.stage_slot = -1;
+        sh.ostage_slot = -1;
     }
     __syncthreads();
 
@@ -2986,7 +3059,7 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
         case 0: break;
         case 1: ok = op_qkv(p, sh, act, ins, c, tim); break;
         case 2: ok = op_partial_attn(p, sh, act, ins, c, tim); break;
-        case 3: ok = op_attn_reduction(p, sh, ins, c, tim); break;
+        case 3: ok = op_attn_reduction(p, sh, act, ins, c, tim); break;
         case 4: ok = op_oproj(p, sh, act, ins, c, tim); break;
         case 5: ok = op_dense_upgate(p, sh, act, ins, c, tim); break;
         case 6: ok = op_dense_down(p, sh, act, ins, c, tim); break;

@@ -18,6 +18,13 @@ the logits for the next launch (``reset_for_next_launch``), so a step after
 the first enqueues the launch alone (``reset_next=False`` keeps the fills).
 ``device_argmax=False`` restores the torch calls and the fills.
 
+Mixtral launches run with ``work_sharing`` on unless the caller says
+otherwise: a workgroup that has finished its own opcode-5 rows takes the
+last rows of the other workers of its group (one per XCD), which evens out
+the XCDs' different streaming rates within each layer; every row is
+computed the same way by whoever takes it, so the results are bit-identical
+to a launch without it.
+
 The schedule is built once (``make_dag`` over all layers plus the LM head)
 and reused for every position; partial-attention instructions cover the
 positions ``[0, pos_id]`` of their partition at run time.
@@ -37,7 +44,7 @@ import time
 
 import torch
 
-from ..scheduler import Schedule, assign_to_sms, tensorize_instructions
+from ..scheduler import Schedule, assign_to_sms, group_rows_by_xcd, tensorize_instructions
 from .mk import MixtralMK_Interpreter
 from .scheduler import make_dag, make_globals
 
@@ -65,7 +72,7 @@ class MK_Generator:
 
     @classmethod
     def build(cls, model, prompt_len: int, mode: str = "rr", sm_count: int | None = None, dag_kwargs=None,
-              globals_kwargs=None, **launch_kwargs):
+              globals_kwargs=None, xcd_rows=(), **launch_kwargs):
         """Globals for ``model`` with the KV cache filled up to ``prompt_len``
         positions, the whole-model schedule assigned with ``mode``, and a
         generator over it.  The model type picks the VM: a model with
@@ -83,11 +90,15 @@ class MK_Generator:
             interpreter = LatencyMK_Interpreter()
         else:
             dag_fn, globals_fn, interpreter = make_dag, make_globals, MixtralMK_Interpreter()
+            launch_kwargs.setdefault("work_sharing", True)
         globs = globals_fn(model, seq_len=prompt_len, sm_count=sm_count, **(globals_kwargs or {}))
         globs.pos_id = prompt_len
         nodes, end = dag_fn(globs, **(dag_kwargs or {}))
         schedule = Schedule(globs, nodes, end)
-        tensorize_instructions(globs, assign_to_sms(mode, schedule=schedule))
+        queues = assign_to_sms(mode, schedule=schedule)
+        if xcd_rows:
+            queues = group_rows_by_xcd(queues, xcd_rows)
+        tensorize_instructions(globs, queues)
         return cls(model, interpreter, schedule, **launch_kwargs)
 
     def fill(self):

@@ -205,6 +205,38 @@ def assign_to_sms(
     raise ValueError(f"Unknown mode: {mode}")
 
 
+def _row_start(ins: Instruction) -> int:
+    for name in ("start_block_idx", "start_output_block_idx"):
+        if hasattr(ins, name):
+            return getattr(ins, name)
+    raise ValueError(f"{type(ins).__name__} has no start block")
+
+
+def group_rows_by_xcd(queues: list[list[Instruction]], opcodes, xcds: int = 8) -> list[list[Instruction]]:
+    """MI355X placement (no reference counterpart): the workgroup of worker
+    w runs on XCD ``w % xcds``.  For each opcode in ``opcodes`` and layer,
+    the instructions keep their queue positions but trade row ranges, so
+    that the workers of one XCD take one contiguous span of rows: the
+    instructions in row order go to the positions ordered by (XCD, worker,
+    queue slot).  Every position keeps an instruction of the same opcode and
+    layer, so the queues' structure and the barrier counts are unchanged;
+    only which worker streams which rows changes (instructions of one
+    opcode and layer need not have equal block counts)."""
+    opcodes = tuple(opcodes)
+    slots: dict[tuple[int, int], list[tuple[int, int]]] = {}
+    for w, q in enumerate(queues):
+        for i, ins in enumerate(q):
+            if ins.opcode() in opcodes:
+                slots.setdefault((ins.opcode(), ins.layer_idx), []).append((w, i))
+    out = [list(q) for q in queues]
+    for pos in slots.values():
+        items = sorted((queues[w][i] for w, i in pos), key=_row_start)
+        order = sorted(pos, key=lambda wi: (wi[0] % xcds, wi[0] // xcds, wi[1]))
+        for ins, (w, i) in zip(items, order):
+            out[w][i] = ins
+    return out
+
+
 def serialize_and_pad(instruction: Instruction) -> list[int]:
     words = instruction.serialize()
     if len(words) > INTS_PER_INSTRUCTION:

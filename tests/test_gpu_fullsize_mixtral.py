@@ -15,7 +15,9 @@ same shapes are checked against the oracle in test_gpu_configs.py):
 * a relaunch from the same input is bit-identical (token, logits, residual,
   the appended K/V rows): the Mixtral path adds in a fixed order; so is a
   launch with prefetch off (``late_loads``: no load before its wait, no
-  predicted expert rows staged in LDS), which reads the same values later;
+  predicted expert rows staged in LDS), which reads the same values later,
+  and one with work sharing (idle workers take other workers' last
+  opcode-5 rows, each computed the same way);
 * the logits are finite and not all zero.
 
 Config 4 decodes at position 4096 and config 5 at 16384 (predictor weights =
@@ -103,5 +105,15 @@ def test_fullsize_decode_properties(model, pos):
             "pred": g.predicted_expert_indices.cpu()}
     for k in first:
         assert torch.equal(first[k], late[k]), f"prefetch off changed {k}"
+    # idle workers taking other workers' opcode-5 rows compute each row the
+    # same way: bit-identical again
+    tok4 = _launch(gen, 1234, pos, work_sharing=True)
+    assert int(tok4) == int(tok)
+    assert torch.equal(g.barriers.cpu(), expected_barriers(g, nparts)), "work sharing: barrier tensor differs"
+    shared = {"logits": g.logits.cpu(), "hidden": g.hidden_states.cpu(), "k": g.k_cache[:, 0, pos].cpu(),
+              "v": g.v_cache[:, 0, pos].cpu(), "sel": g.selected_expert_indices.cpu(),
+              "pred": g.predicted_expert_indices.cpu()}
+    for k in first:
+        assert torch.equal(first[k], shared[k]), f"work sharing changed {k}"
     print(f"[fullsize pos {pos}] token {int(tok)}, last layer experts {first['sel'].tolist()} "
           f"(predicted {first['pred'].tolist()})", flush=True)
