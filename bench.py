@@ -654,6 +654,8 @@ def main():
     ap.add_argument("--layer-steps", type=int, default=10,
                     help="c4: timed steps (of --tokens launches) of the config-2 layer figures")
     ap.add_argument("--no-layer", action="store_true", help="c4: leave out the config-2 layer figures")
+    ap.add_argument("--layer-after", action="store_true",
+                    help="c4: time the config-2 layer after the decode run instead of before it")
     ap.add_argument("--assign", default="rr", choices=["rr", "zz", "wave", "dag"],
                     help="c3/c4/c5: instruction-to-worker assignment of the whole-model schedule")
     ap.add_argument("--qkv-block", type=int, default=0,
@@ -731,6 +733,13 @@ def main():
     warmup = max(1, args.warmup)
     if args.config in ("c3", "c4", "c5"):
         steps = args.steps or args.decode_steps or (256 if args.config == "c3" else 128)
+        layer_fig = None
+        if args.config == "c4" and not args.no_layer and not args.layer_after:
+            # the config-2 layer first, on a device that has not yet held the
+            # 94 GB model
+            layer_fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
+            del bench
+            torch.cuda.empty_cache()
         out, model, gen = decode_bench(args, args.config, steps, warmup)
         if args.config == "c4" and not args.no_cpu:
             print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)", file=sys.stderr,
@@ -739,11 +748,12 @@ def main():
                                                       gen.schedule.globs.sm_count())
         del model, gen
         torch.cuda.empty_cache()
-        if args.config == "c4" and not args.no_layer:
-            fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
-            out["moe_layer"] = fig
+        if args.config == "c4" and not args.no_layer and args.layer_after:
+            layer_fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
             del bench
             torch.cuda.empty_cache()
+        if layer_fig is not None:
+            out["moe_layer"] = layer_fig
         print(json.dumps(out), flush=True)
         return
 
