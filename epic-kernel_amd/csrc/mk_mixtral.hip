@@ -309,6 +309,14 @@ __device__ __forceinline__ u32x4 ld_dev128(const void *base, uint32_t byte_off) 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
     return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCachePolicySc1);
 }
+// 4-byte device-coherent load of base + byte_off (base uniform across the
+// wave) as a raw buffer load with the sc1 policy: unlike an atomic load,
+// the compiler may issue many of them back to back.
+__device__ __forceinline__ uint32_t ld_dev32_at(const void *base, uint32_t byte_off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kCachePolicySc1);
+}
 __device__ __forceinline__ void st_dev128(u32x4 *p, u32x4 v) {
     uint32_t *q = reinterpret_cast<uint32_t *>(p);
     st_dev32(q, v.x);
@@ -2047,6 +2055,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, Shared
             for (int j = 0; j < 8; ++j) wacc[(wave * GQA + h) * D + dp * 8 + j] = acc[h][j];
     }
     __syncthreads();
+    stamp(tim, 55);  // every wave's partials are in LDS
     for (int i = threadIdx.x; i < GQA * D; i += kThreads) {
         const int h = i / D, d = i % D;
         float Mx = -INFINITY;
@@ -2072,6 +2081,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, Shared
             }
         }
     }
+    stamp(tim, 56);  // thread 0's merged outputs stored
     drain_and_sync();
     if (a.skip_red)
         arrive(p, bar_at(p, layer, 3), GQA);
@@ -2144,10 +2154,18 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
     if (!need_attention(p, c, 3, layer)) return false;
     attn_c &a = attn_of(p);  // valid: attention tensors are present
     const int gqa = a.Hq / a.Hkv;
-    const int out_slot = (n >= 0 && n <= MK_INTS_PER_INSTRUCTION - 7) ? __builtin_amdgcn_readfirstlane(ins[6 + n]) : -1;
-    bool bad = layer < 0 || layer >= p.num_layers || hs < 0 || hs + gqa > a.Hq || n < 1 ||
-               n > MK_INTS_PER_INSTRUCTION - 7 || (!terminal && (out_slot < 0 || out_slot >= a.P));
-    for (int i = 0; !bad && i < n; ++i) {
+    // n < 0: the list is the range of partial slots 0 .. -n - 1, for more
+    // partials than a 32-word instruction can list (no reference
+    // counterpart: its lists stop at 25, demos/mixtral/mixtral.cuh)
+    const bool range = n < 0;
+    const int cnt = range ? -n : n;
+    const int out_slot = range ? __builtin_amdgcn_readfirstlane(ins[6])
+                         : n <= MK_INTS_PER_INSTRUCTION - 7 ? __builtin_amdgcn_readfirstlane(ins[6 + n])
+                                                            : -1;
+    bool bad = layer < 0 || layer >= p.num_layers || hs < 0 || hs + gqa > a.Hq || cnt < 1 ||
+               (range ? cnt > 64 || cnt > a.P : n > MK_INTS_PER_INSTRUCTION - 7) ||
+               (!terminal && (out_slot < 0 || out_slot >= a.P));
+    for (int i = 0; !bad && !range && i < n; ++i) {
         const int s = ins[6 + i];
         bad = s < 0 || s >= a.P;
     }
@@ -2165,34 +2183,40 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
     static_assert(kRowBatchLds * 2 * kMaxSegments >= 4 * 64 + 4 + 64, "reduction staging fits in sh.part");
     float *wts = reinterpret_cast<float *>(sh.part);  // [gqa][64]
     float *den = wts + 4 * 64;                        // [gqa]
-    int *slots = reinterpret_cast<int *>(den + 4);    // [n]
+    int *slots = reinterpret_cast<int *>(den + 4);    // [cnt]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (wave < gqa) {
-        const int s = lane < n ? ins[6 + lane] : 0;
-        float lse = lane < n ? __uint_as_float(ld_dev32(a.lse_int + (size_t)(hs + wave) * a.P + s)) : -INFINITY;
+        const int s = lane < cnt ? (range ? lane : ins[6 + lane]) : 0;
+        float lse = lane < cnt ? __uint_as_float(ld_dev32(a.lse_int + (size_t)(hs + wave) * a.P + s)) : -INFINITY;
         float mx = lse;
         for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float f = lane < n ? exp2f(lse - mx) : 0.f;
+        const float f = lane < cnt ? exp2f(lse - mx) : 0.f;
         const float tot = wave_sum(f);
         wts[wave * 64 + lane] = f;
         if (lane == 0) den[wave] = tot;
-        if (wave == 0 && lane < n) slots[lane] = s;
+        if (wave == 0 && lane < cnt) slots[lane] = s;
     }
     __syncthreads();
+    stamp(tim, 52);  // the weights are in LDS
     for (int i = threadIdx.x; i < gqa * D; i += kThreads) {
         const int hl = i / D, h = hs + hl, d = i % D;
-        const float *out = a.out_int + (size_t)h * a.P * D + d;
         const float *f = wts + hl * 64;
         float num = 0.f;
-        int k = 0;
-        for (; k + 8 <= n; k += 8) {
-            float v[8];
+        // the partials in groups of 32 loads in flight (one round trip for up
+        // to 32 partitions): every slot index first, then every load; a
+        // group's missing entries load the last slot again and add nothing
+        for (int k = 0; k < cnt; k += 32) {
+            int sl[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = __uint_as_float(ld_dev32(out + (size_t)slots[k + u] * D));
+            for (int u = 0; u < 32; ++u) sl[u] = range ? min(k + u, cnt - 1) : slots[min(k + u, cnt - 1)];
+            float v[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) num = fmaf(v[u], f[k + u], num);
+            for (int u = 0; u < 32; ++u)
+                v[u] = __uint_as_float(ld_dev32_at(a.out_int, (uint32_t)(((h * a.P + sl[u]) * D + d) * 4)));
+#pragma unroll
+            for (int u = 0; u < 32; ++u)
+                if (k + u < cnt) num = fmaf(v[u], f[k + u], num);
         }
-        for (; k < n; ++k) num = fmaf(__uint_as_float(ld_dev32(out + (size_t)slots[k] * D)), f[k], num);
         const float red = num / den[hl];
         if (terminal) {
             st_dev16(a.attn_out + h * D + d, f2bf(red));
@@ -2201,6 +2225,7 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
             if (d == 0) st_dev32(a.lse_int + (size_t)h * a.P + out_slot, __float_as_uint(logf(den[hl])));
         }
     }
+    stamp(tim, 53);  // thread 0's sums done and stored
     drain_and_sync();
     arrive(p, bar_at(p, layer, 3), gqa);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);

@@ -139,6 +139,27 @@ class Instruction:
         return words
 
 
+#: partials a reduction instruction lists explicitly: its 32-word instruction
+#: holds 7 other words
+MAX_LISTED_PARTIALS = 25
+
+
+def serialize_reduction(ins) -> list[int]:
+    """Words of an attention-reduction instruction (opcode 3): the
+    reference's layout (``[3, layer, head_start, num_partials, is_terminal,
+    n, list..., output_partial_idx]``) while the list fits the 32-word
+    instruction (MAX_LISTED_PARTIALS entries).  A longer list that is the
+    range ``0 .. n - 1`` is written as ``-n`` with no entries (no reference
+    counterpart: the MI355X partition policy splits the cache over up to 64
+    partitions per KV head); any other longer list is an error."""
+    n = len(ins.reduction_list)
+    if n > MAX_LISTED_PARTIALS and list(ins.reduction_list) == list(range(n)):
+        out = 0 if ins.output_partial_idx is None else int(ins.output_partial_idx)
+        return [int(ins.opcode()), int(ins.layer_idx), int(ins.head_start_idx), int(ins.num_partials),
+                int(ins.is_terminal), -n, out]
+    return Instruction.serialize(ins)
+
+
 @dataclass
 class NoOp(Instruction):
     @classmethod

@@ -19,7 +19,7 @@ from typing import Optional
 
 from torch import Tensor
 
-from ..instructions import BaseGlobals, Instruction
+from ..instructions import BaseGlobals, Instruction, serialize_reduction
 
 
 @dataclass
@@ -106,6 +106,9 @@ class AttentionReduction(Instruction):
 
     def cost(self, globs: Globals):
         return globs.num_attention_heads // globs.num_kv_heads * self.num_partials * globs.head_dim
+
+    def serialize(self) -> list[int]:
+        return serialize_reduction(self)
 
 
 @dataclass

@@ -33,7 +33,7 @@ from typing import Optional
 
 from torch import Tensor
 
-from ..instructions import BaseGlobals, Instruction
+from ..instructions import BaseGlobals, Instruction, serialize_reduction
 
 OPCODE_QKV = 1
 OPCODE_PARTIAL_ATTN = 2
@@ -153,6 +153,9 @@ class Mixtral_AttnReduction(Instruction):
 
     def cost(self, globs: MixtralGlobals) -> float:
         return globs.num_attention_heads // globs.num_kv_heads * self.num_partials * globs.head_dim
+
+    def serialize(self) -> list[int]:
+        return serialize_reduction(self)
 
 
 @dataclass

@@ -22,8 +22,8 @@ Differences, all MI355X-motivated and recorded here:
   Passing ``16`` reproduces the reference partition.  The oracle reads the
   block sizes from the globals, so results do not depend on this choice.
 * the split-KV partition count defaults to the MI355X policy of
-  :func:`pick_num_attention_partitions` (chunks of >= 112 positions, up to 25
-  partitions per KV head) instead of the reference's (>= 256 positions, at
+  :func:`pick_num_attention_partitions` (chunks of >= 112 positions, up to
+  min(W / kv_heads, 64) partitions per KV head) instead of the reference's (>= 256 positions, at
   most 160 / kv_heads): the kernel's partial attention is VALU-bound per
   workgroup, so more, shorter partitions finish sooner.
   ``attention_partitions="reference"`` reproduces the reference partition.
@@ -70,8 +70,12 @@ BARRIER_OPS = 10
 #: reference cap on attention partitions per layer (mkm/scheduler.py:21)
 ATTN_PARTITION_CAP = 160
 #: partials a terminal reduction can list: its 32-word instruction holds 7
-#: other words
+#: other words (the reference's partition policies stay within it)
 MAX_REDUCTION_LIST = 25
+#: partitions per KV head of the MI355X policy: a terminal reduction over
+#: more than MAX_REDUCTION_LIST partials is encoded as a range (one lane per
+#: partial in the kernel's reduction: 64 at most)
+MAX_PARTITIONS = 64
 #: fewest positions per partition of the MI355X policy (swept at config 3:
 #: 17-19 partitions of 112-128 positions beat 22 of 96 by 1.5 %, and 13-15 by
 #: 2 %; configs 4 and 5 stay at the cap)
@@ -86,26 +90,31 @@ def pick_num_attention_partitions(prompt_len: int, ntok: int, num_kv_heads: int,
     positions, at most ``min(W, 160) // kv_heads`` partitions.
 
     ``"mi355x"``: chunks of at least 112 positions and at most ``min(W //
-    kv_heads, 25)`` partitions, trimmed so that none is empty.  A
+    kv_heads - 1, 64)`` partitions (one worker per KV head is left for its
+    reduction), trimmed so that none is empty.  A
     workgroup's partial attention is bound by how fast it pulls its K/V rows
     (and, for short partitions, by its fixed merge-and-store cost), not by
     the HBM bandwidth of the whole chip, so on 256 compute units it pays to
-    spread the cache over more of them; 25 is what one terminal reduction
-    instruction can list.  ``"mi355x:N"`` caps the count at N instead.
+    spread the cache over all of them.  More than 25 partials (what one
+    reduction instruction lists) are reduced through a range-encoded list
+    (``Mixtral_AttnReduction.serialize``).  ``"mi355x:N"`` caps the count at
+    N instead.
     """
     seq = prompt_len + ntok
     if policy == "reference":
         chunks = math.ceil(seq / 256)
         cap = min(sm_count, ATTN_PARTITION_CAP) // num_kv_heads
         return max(1, min(chunks, cap))
-    cap = MAX_REDUCTION_LIST
+    cap = MAX_PARTITIONS
     if policy.startswith("mi355x:"):
         cap = int(policy.split(":", 1)[1])
-        if not 1 <= cap <= MAX_REDUCTION_LIST:
-            raise ValueError(f"partition cap must be in 1..{MAX_REDUCTION_LIST}, got {cap}")
+        if not 1 <= cap <= MAX_PARTITIONS:
+            raise ValueError(f"partition cap must be in 1..{MAX_PARTITIONS}, got {cap}")
     elif policy != "mi355x":
         raise ValueError(f"unknown partition policy {policy!r}")
-    n = max(1, min(math.ceil(seq / MIN_PARTITION_POSITIONS), sm_count // num_kv_heads, cap))
+    # one worker per KV head stays free of partials for its reduction, which
+    # then waits while the partials run instead of starting after one
+    n = max(1, min(math.ceil(seq / MIN_PARTITION_POSITIONS), sm_count // num_kv_heads - 1, cap))
     total = math.ceil(seq / kv_block_size)
     return max(1, math.ceil(total / math.ceil(total / n)))
 

@@ -118,6 +118,10 @@ enum {
      * the ones selected, one byte each (predicted 0, 1, selected 0, 1 from
      * the low byte up; 0xff = no prediction) -- not a time */
     MK_TEVENT_PREDICTION = 50
+    /* also written, as times: 52-53 inside opcode 3 (weights in LDS, sums
+     * stored), 55-56 inside opcode 2 (wave partials in LDS, merged outputs
+     * stored), 60-63 inside the RMSNorm + router of opcodes 5 and 8, 64-95
+     * per-item completions of opcode 5 (waves 0 and 7, 16 items each) */
 };
 
 typedef struct mk_mixtral_globals {

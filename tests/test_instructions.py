@@ -64,8 +64,12 @@ def test_serialize_words():
     assert Mixtral_RMS_LM_Head(1, 2).serialize() == [7, 1, 2, 0]
     padded = serialize_and_pad(RmsRouterUpgate(3, 10, 7))
     assert len(padded) == INTS_PER_INSTRUCTION and padded[:4] == [5, 3, 10, 7] and not any(padded[4:])
+    # more partials than a 32-word instruction lists: the range 0 .. n - 1 is
+    # written as -n (an MI355X extension); any other long list is an error
+    assert serialize_and_pad(Mixtral_AttnReduction(2, 4, 40, True, list(range(40))))[:8] == [3, 2, 4, 40, 1, -40, 0, 0]
+    assert Mixtral_AttnReduction(0, 0, 25, True, list(range(25))).serialize()[5:7] == [25, 0]
     with pytest.raises(ValueError):
-        serialize_and_pad(Mixtral_AttnReduction(0, 0, 40, True, list(range(40))))
+        serialize_and_pad(Mixtral_AttnReduction(0, 0, 40, True, list(range(1, 41))))
 
 
 def test_round_robin_and_zig_zag():

@@ -142,22 +142,22 @@ def test_dag_structure(policy, parts):
 @pytest.mark.parametrize("seq,kv,W", [(1, 8, 256), (64, 8, 256), (65, 8, 256), (2049, 8, 256), (4097, 8, 256),
                                       (16385, 8, 256), (301, 4, 16), (1000, 2, 7)])
 def test_mi355x_partition_policy(seq, kv, W):
-    """At most min(W / kv, 25) partitions, none empty, more than 56
+    """At most min(W / kv - 1, 64) partitions, none empty, more than 56
     positions each on average (n = ceil(seq / 112) before the cap); the
     reference policy is unchanged; "mi355x:N" caps the count at N."""
     from megakernels_amd.mixtral.scheduler import pick_num_attention_partitions
     from oracle.python_vm import partial_token_range
 
     n = pick_num_attention_partitions(seq, 0, kv, W, "mi355x")
-    assert 1 <= n <= max(1, min(W // kv, 25))
+    assert 1 <= n <= max(1, min(W // kv - 1, 64))
     ranges = [partial_token_range(seq, 16, n, p) for p in range(n)]
     assert all(b > a for a, b in ranges)
     assert [t for a, b in ranges for t in range(a, b)] == list(range(seq))
-    if n < min(W // kv, 25):
+    if n < min(W // kv - 1, 64):
         assert n == 1 or seq / n > 56
-    for cap in (1, 8, 25):
+    for cap in (1, 8, 25, 64):
         assert pick_num_attention_partitions(seq, 0, kv, W, f"mi355x:{cap}") <= cap
     with pytest.raises(ValueError):
-        pick_num_attention_partitions(seq, 0, kv, W, "mi355x:26")
+        pick_num_attention_partitions(seq, 0, kv, W, "mi355x:65")
     ref = pick_num_attention_partitions(seq, 0, kv, W)
     assert ref == max(1, min(math.ceil(seq / 256), min(W, 160) // kv))
