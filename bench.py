@@ -45,12 +45,14 @@ for p in (ROOT / "epic-kernel_amd", ROOT):
 
 METRIC = "batch-1 decode tokens/s, Mixtral-8x7B shape; MoE layer µs; % HBM peak"
 HBM_PEAK_GBS = 8000.0
-# HBM bytes moved per launch of mk_mixtral_kernel at config 2: rocprofv3
-# FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the same counter
-# reads for a device copy of known size (FETCH x 2.0, WRITE x 1.0); the
-# counter runs are summarised under profiles/.
-MEASURED_TRAFFIC_BYTES = {"c2": 708_573_701}
-TRAFFIC_UNIT = "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+# HBM bytes moved per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE per
+# dispatch, each scaled by what the same counter reads for a device copy of
+# known size: FETCH x 2.0, WRITE x 1.0), measured on commit 7794364: config 2
+# one MoE layer; configs 3/4/5 one decode step at 2050 / 4098 / 16386 cached
+# positions.  The counter runs are summarised under profiles/.
+MEASURED_TRAFFIC_BYTES = {"c2": 708_914_009, "c3": 6_741_897_441, "c4": 26_355_159_089, "c5": 27_959_777_772}
+TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, commit 7794364; configs 3-5 "
+                "at 2050 / 4098 / 16386 cached positions)")
 
 
 def moe_layer_bytes(cfg) -> int:
