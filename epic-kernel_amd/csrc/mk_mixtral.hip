@@ -227,6 +227,10 @@ struct KParams {
     int32_t *spread;
     int32_t spread_rows, spread_stride;
     int32_t spread_ops;  // bit k: rows of opcode k are spread
+    // exact division by bar_width and bar_ops for barrier offsets below
+    // bar_ints (< 2^16 whenever spread is set): q = umulhi(n, ceil(2^32 / d))
+    uint32_t bar_width_magic, bar_ops_magic;
+    int32_t bar_ints;
     AttnParams attn_params;  // read only through attn_of()
 };
 
@@ -430,12 +434,19 @@ __device__ __forceinline__ void report_error(const KParams &p, int code, const C
 
 // Row of the spread counter table for `ctr` (the counter at index 0 of a
 // (layer, opcode) row of the barrier tensor), or -1 (not spread).
+// Divisions by the barrier tensor's row lengths are multiplications by
+// host-computed reciprocals (exact for n, d < 2^16: the error n (m d - 2^32)
+// / (d 2^32) stays below 1 / d), a few scalar instructions where a 64-bit
+// division would take some 150 at every arrival and wait.
 __device__ __forceinline__ int spread_row(const KParams &p, const int32_t *ctr) {
     if (p.spread == nullptr) return -1;
-    const long off = ctr - p.bar;
-    if (off < 0 || off % p.bar_width != 0) return -1;
-    const long row = off / p.bar_width;
-    if (row >= p.spread_rows || !((p.spread_ops >> (row % p.bar_ops + 1)) & 1)) return -1;
+    const long d = ctr - p.bar;
+    if (d < 0 || d >= p.bar_ints) return -1;
+    const uint32_t off = (uint32_t)d;
+    const uint32_t row = __umulhi(off, p.bar_width_magic);
+    if (row * (uint32_t)p.bar_width != off || (int)row >= p.spread_rows) return -1;
+    const uint32_t op0 = row - __umulhi(row, p.bar_ops_magic) * (uint32_t)p.bar_ops;
+    if (!((p.spread_ops >> (op0 + 1)) & 1)) return -1;
     return (int)row;
 }
 
@@ -3322,6 +3333,18 @@ uint32_t timeout_ticks(uint32_t spin_timeout_us) {
     return ticks > 0xffffffffu ? 0xffffffffu : (uint32_t)ticks;
 }
 
+// ceil(2^32 / d) for d >= 2: spread_row's exact division of n < 2^16 by d < 2^16.
+uint32_t div_magic(int32_t d) { return d >= 2 ? (uint32_t)(((1ull << 32) + (uint64_t)d - 1) / (uint64_t)d) : 0u; }
+
+// Divisors of spread_row; spreading stays off where they would not be exact.
+void set_spread_divisors(KParams &kp, int64_t layers) {
+    const int64_t ints = layers * (int64_t)kp.bar_ops * (int64_t)kp.bar_width;
+    kp.bar_width_magic = div_magic(kp.bar_width);
+    kp.bar_ops_magic = div_magic(kp.bar_ops);
+    kp.bar_ints = (int32_t)std::min<int64_t>(ints, 1 << 16);
+    if (ints >= (1 << 16) || kp.bar_width < 2 || kp.bar_ops < 2) kp.spread = nullptr;
+}
+
 // Dynamic LDS for the launch with an opcode-2 ring of `kv_ring` chunks
 // (ignored without attention tensors).
 size_t lds_bytes_for(const mk_mixtral_globals *g, int kv_ring) {
@@ -3547,6 +3570,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.E = 1;
     kp.bar_ops = (int32_t)g->bar_ops;
     kp.bar_width = (int32_t)g->bar_width;
+    set_spread_divisors(kp, g->num_layers);
     kp.expert_bs = g->up_gate_proj_block_size;
     kp.down_bs = g->down_proj_block_size;
     kp.oproj_bs = g->o_proj_block_size;
@@ -3711,6 +3735,7 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.E = g->num_experts;
     kp.bar_ops = (int32_t)g->bar_ops;
     kp.bar_width = (int32_t)g->bar_width;
+    set_spread_divisors(kp, g->num_layers);
     kp.expert_bs = g->expert_proj_block_size;
     kp.down_bs = g->down_proj_block_size;
     kp.oproj_bs = g->o_proj_block_size;
