@@ -242,10 +242,21 @@ struct KParams {
     AttnParams attn_params;  // read only through attn_of()
 };
 
+// The launch parameters, read in place from the kernel-argument segment
+// (KParams is the kernel's only argument, at offset 0): scalar loads where a
+// field is used, instead of every field held in registers for the whole
+// persistent loop.
+typedef const __attribute__((address_space(4))) KParams kp_c;
+__device__ __forceinline__ kp_c &kparams() {
+    const __attribute__((address_space(4))) char *kernarg =
+        (const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr();
+    return *reinterpret_cast<kp_c *>(kernarg);
+}
+
 // The launch's attention parameters, addressed in the kernel-argument
 // segment itself (KParams is the kernel's only argument, at offset 0).
 typedef const __attribute__((address_space(4))) AttnParams attn_c;
-__device__ __forceinline__ attn_c &attn_of(const KParams &) {
+__device__ __forceinline__ attn_c &attn_of(kp_c &) {
     const __attribute__((address_space(4))) char *kernarg =
         (const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr();
     return *reinterpret_cast<attn_c *>(kernarg + offsetof(KParams, attn_params));
@@ -412,16 +423,16 @@ __device__ __forceinline__ void stamp(int32_t *t, int slot) {
     if (t != nullptr && threadIdx.x == 0) t[slot] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
 }
 
-__device__ __forceinline__ int32_t *bar_at(const KParams &p, int layer, int opcode) {
+__device__ __forceinline__ int32_t *bar_at(kp_c &p, int layer, int opcode) {
     return p.bar + ((size_t)layer * p.bar_ops + (opcode - 1)) * p.bar_width;
 }
 
-__device__ __forceinline__ bool aborted(const KParams &p) {
+__device__ __forceinline__ bool aborted(kp_c &p) {
     return __hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
 // Record the first failure; called by one lane.
-__device__ __forceinline__ void report_error_lane(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected,
+__device__ __forceinline__ void report_error_lane(kp_c &p, int code, const Ctx &c, int opcode, int layer, int expected,
                                   int seen) {
     int zero = 0;
     if (__hip_atomic_compare_exchange_strong(p.status, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
@@ -436,7 +447,7 @@ __device__ __forceinline__ void report_error_lane(const KParams &p, int code, co
 }
 
 // Record the first failure (thread 0 of the reporting workgroup only).
-__device__ __forceinline__ void report_error(const KParams &p, int code, const Ctx &c, int opcode, int layer, int expected, int seen) {
+__device__ __forceinline__ void report_error(kp_c &p, int code, const Ctx &c, int opcode, int layer, int expected, int seen) {
     if (threadIdx.x == 0) report_error_lane(p, code, c, opcode, layer, expected, seen);
 }
 
@@ -446,7 +457,7 @@ __device__ __forceinline__ void report_error(const KParams &p, int code, const C
 // host-computed reciprocals (exact for n, d < 2^16: the error n (m d - 2^32)
 // / (d 2^32) stays below 1 / d), a few scalar instructions where a 64-bit
 // division would take some 150 at every arrival and wait.
-__device__ __forceinline__ int spread_row(const KParams &p, const int32_t *ctr) {
+__device__ __forceinline__ int spread_row(kp_c &p, const int32_t *ctr) {
     if (p.spread == nullptr) return -1;
     const long d = ctr - p.bar;
     if (d < 0 || d >= p.bar_ints) return -1;
@@ -463,20 +474,20 @@ __device__ __forceinline__ int spread_row(const KParams &p, const int32_t *ctr) 
 // applies those atomics one at a time (~15 ns each): the last of 256
 // O-projection arrivals landed ~4 us after the stage ended.  A spread
 // counter's arrivals go to this XCD's part instead, 32 per part.
-__device__ __forceinline__ void arrive_add(const KParams &p, int32_t *ctr, int n) {
+__device__ __forceinline__ void arrive_add(kp_c &p, int32_t *ctr, int n) {
     const int row = spread_row(p, ctr);
     int32_t *dst = row < 0 ? ctr : p.spread + (size_t)(blockIdx.x % kSpread) * p.spread_stride + row;
     __hip_atomic_fetch_add(dst, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void arrive(const KParams &p, int32_t *ctr, int n) {
+__device__ __forceinline__ void arrive(kp_c &p, int32_t *ctr, int n) {
     if (threadIdx.x == 0) arrive_add(p, ctr, n);
 }
 
 // Current value of counter `ctr` (row `row` of the spread table, or -1),
 // read by one lane: the counter and its kSpread parts, all loads in flight
 // together.
-__device__ __forceinline__ int counter_value(const KParams &p, const int32_t *ctr, int row) {
+__device__ __forceinline__ int counter_value(kp_c &p, const int32_t *ctr, int row) {
     int v = (int)ld_dev32(ctr);
     if (row >= 0) {
         uint32_t part[kSpread];
@@ -490,7 +501,7 @@ __device__ __forceinline__ int counter_value(const KParams &p, const int32_t *ct
 
 // Whether counter `ctr` has reached `expected`, for the workgroup (thread 0
 // reads it; ends with a workgroup barrier).
-__device__ __forceinline__ bool counter_reached(const KParams &p, SharedState &sh, const int32_t *ctr, int expected) {
+__device__ __forceinline__ bool counter_reached(kp_c &p, SharedState &sh, const int32_t *ctr, int expected) {
     if (threadIdx.x == 0) sh.flag = counter_value(p, ctr, spread_row(p, ctr)) >= expected;
     __syncthreads();
     const bool r = sh.flag != 0;
@@ -501,7 +512,7 @@ __device__ __forceinline__ bool counter_reached(const KParams &p, SharedState &s
 // Wait until counter `ctr` >= expected.  Thread 0 spins; the result is
 // broadcast.  Returns false (uniformly) on time-out or when another worker
 // has failed.
-__device__ __forceinline__ bool wait_ge(const KParams &p, SharedState &sh, int32_t *ctr, int expected, const Ctx &c, int opcode,
+__device__ __forceinline__ bool wait_ge(kp_c &p, SharedState &sh, int32_t *ctr, int expected, const Ctx &c, int opcode,
                         int layer) {
     if (threadIdx.x == 0) {
         const int row = spread_row(p, ctr);
@@ -608,7 +619,7 @@ __device__ __forceinline__ void pair_ahead_load(PairAhead &r, const uint16_t *ma
 
 // Byte offset in the dynamic LDS of the 8 KiB (1 KiB per wave) that the
 // opcode-6 cache warming writes into: after the SiLU staging area.
-__device__ __forceinline__ uint32_t lds_prefetch_offset(const KParams &p) {
+__device__ __forceinline__ uint32_t lds_prefetch_offset(kp_c &p) {
     return (uint32_t)p.F * 4u;
 }
 
@@ -622,7 +633,7 @@ __device__ __forceinline__ uint32_t lds_prefetch_offset(const KParams &p) {
 template <int kE>
 struct Experts {
     static constexpr int kMax = kE > 0 ? kE : MK_MAX_EXPERTS;
-    __device__ static __forceinline__ bool has(const KParams &p, int e) { return kE > 0 ? e < kE : e < p.E; }
+    __device__ static __forceinline__ bool has(kp_c &p, int e) { return kE > 0 ? e < kE : e < p.E; }
 };
 
 // Per-thread norm weights and router rows, loaded before the producer wait
@@ -635,10 +646,10 @@ struct RouterRegs {
     u32x4 rw[Experts<kE>::kMax];
 };
 
-__device__ __forceinline__ bool router_fits(const KParams &p) { return (p.H >> 3) <= kThreads; }
+__device__ __forceinline__ bool router_fits(kp_c &p) { return (p.H >> 3) <= kThreads; }
 
 template <int kE>
-__device__ __forceinline__ void router_prefetch(const KParams &p, SharedState &sh, int layer, const uint16_t *router,
+__device__ __forceinline__ void router_prefetch(kp_c &p, SharedState &sh, int layer, const uint16_t *router,
                                                 RouterRegs<kE> &rr) {
     const int v = threadIdx.x;
     if (v < p.E) sh.bias[v] = p.router_bias != nullptr ? p.router_bias[layer * p.E + v] : 0.f;
@@ -665,7 +676,7 @@ __device__ __forceinline__ float sumsq8(u32x4 x) { return sumsq2(x.x) + sumsq2(x
 // sums the per-wave partials itself, so the logits end up in registers after
 // a single workgroup barrier.
 template <int kE>
-__device__ __forceinline__ void finish_logits(const KParams &p, SharedState &sh, const float *acc, float *logits) {
+__device__ __forceinline__ void finish_logits(kp_c &p, SharedState &sh, const float *acc, float *logits) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int e = 0; e < Experts<kE>::kMax; ++e) {
@@ -690,7 +701,7 @@ __device__ __forceinline__ void finish_logits(const KParams &p, SharedState &sh,
 // normed hidden (bf16) -> act[0 .. H/8); router logits -> logits[0 .. E) in
 // every thread.  Reads hidden_states, so it runs after the producer wait.
 template <int kE>
-__device__ __forceinline__ void rms_router(const KParams &p, SharedState &sh, u32x4 *act, int layer, const uint16_t *router,
+__device__ __forceinline__ void rms_router(kp_c &p, SharedState &sh, u32x4 *act, int layer, const uint16_t *router,
                            const RouterRegs<kE> &rr, int32_t *tim, float *logits) {
     const int tid = threadIdx.x;
     const int nv = p.H >> 3;
@@ -745,7 +756,7 @@ struct Top2 {
 // comparison: the lower expert index wins a tie); p_i = exp(l_i - max) / sum
 // as torch.softmax computes it.
 template <int kE>
-__device__ __forceinline__ Top2 softmax_top2(const KParams &p, const float *logits) {
+__device__ __forceinline__ Top2 softmax_top2(kp_c &p, const float *logits) {
     int i0 = 0;
     float l0 = logits[0];
 #pragma unroll
@@ -784,7 +795,7 @@ __device__ __forceinline__ int next_local_item(SharedState &sh, int lane) {
 
 // silu_out[e][r] = bf16(bf16(silu(bf16 g)) * bf16 u) from the wave sums of
 // the gate and up rows (lane 0 stores).
-__device__ __forceinline__ void silu_store(const KParams &p, int e, int r, float ag, float au, int lane) {
+__device__ __forceinline__ void silu_store(kp_c &p, int e, int r, float ag, float au, int lane) {
     if (lane == 0) {
         const float g = rbf(ag), u = rbf(au);
         const float sg = rbf(g / (1.0f + expf(-g)));
@@ -795,7 +806,7 @@ __device__ __forceinline__ void silu_store(const KParams &p, int e, int r, float
 // One item of opcode 5: row r of the FFN dimension for expert slot j, i.e.
 // the gate and up rows (H bf16 each) dotted with the normed hidden state,
 // then silu_out[e][r] = bf16(bf16(silu(bf16(g))) * bf16(u)).
-__device__ __forceinline__ void upgate_item(const KParams &p, const u32x4 *act, int layer, int row0, int nrows,
+__device__ __forceinline__ void upgate_item(kp_c &p, const u32x4 *act, int layer, int row0, int nrows,
                                             int e0, int e1, int it, int lane) {
     const int j = it >= nrows;
     const int r = row0 + (j ? it - nrows : it);
@@ -810,7 +821,7 @@ __device__ __forceinline__ void upgate_item(const KParams &p, const u32x4 *act, 
 // ones this wave staged in LDS (the predicted top-1 expert's row row0 + it,
 // staged by the preceding O projection; the loads have landed once the wave
 // has waited for its own loads).
-__device__ __forceinline__ void upgate_item_staged(const KParams &p, const u32x4 *act, int row0, int e, int it,
+__device__ __forceinline__ void upgate_item_staged(kp_c &p, const u32x4 *act, int row0, int e, int it,
                                                    int wave, int lane) {
     const int nc = p.H / kChunkElems;
     const u32x4 *sg = act + p.stage_off16 + (wave - 1) * 2 * nc * 64 + lane, *su = sg + nc * 64;
@@ -841,7 +852,7 @@ __device__ __forceinline__ int claim_issue(int32_t *cursor, int lane) {
 // outside the window is only left out of the sharing (its owner still does
 // all of its items); out-of-range operands are left out too (their owner
 // reports them).  The caller's next workgroup barrier publishes the pool.
-__device__ __forceinline__ void pool_scan_near(const KParams &p, SharedState &sh, int layer, int group, int slot) {
+__device__ __forceinline__ void pool_scan_near(kp_c &p, SharedState &sh, int layer, int group, int slot) {
     static_assert(kPoolGroup * kPoolWindow == 64, "pool_scan_near: one slot per lane of wave 0");
     const int lane = threadIdx.x & 63;
     const int w0 = group * kPoolGroup, mate = lane / kPoolWindow;
@@ -865,7 +876,7 @@ __device__ __forceinline__ void pool_scan_near(const KParams &p, SharedState &sh
 
 __device__ __forceinline__ int tail_items(int items) { return items < MK_TAIL_ITEMS ? items : MK_TAIL_ITEMS; }
 
-__device__ __forceinline__ int32_t *slot_cursor(const KParams &p, int slot) {
+__device__ __forceinline__ int32_t *slot_cursor(kp_c &p, int slot) {
     return p.scratch + kScratchSlotBase + 2 * slot;
 }
 
@@ -873,7 +884,7 @@ __device__ __forceinline__ int32_t *slot_cursor(const KParams &p, int slot) {
 // start at row0 (nrows rows, items 0 .. 2*nrows), claimed one at a time from
 // the instruction's cursor (the next claim is issued before the current
 // item's loads) until the cursor passes count.  Returns the number done here.
-__device__ __forceinline__ int upgate_claimed(const KParams &p, const u32x4 *act, int layer, int row0, int nrows, int e0, int e1,
+__device__ __forceinline__ int upgate_claimed(kp_c &p, const u32x4 *act, int layer, int row0, int nrows, int e0, int e1,
                               int first, int count, int32_t *cursor, int lane) {
     int done_here = 0;
     int c = __builtin_amdgcn_readfirstlane(claim_issue(cursor, lane));
@@ -894,7 +905,7 @@ __device__ __forceinline__ int upgate_claimed(const KParams &p, const u32x4 *act
 // instruction completes only after its owner has also published the routing
 // (for the block-0 instruction); the report that reaches items + 1 arrives
 // for the instruction's rows on the layer and chunk counters.
-__device__ __forceinline__ void publish_items(const KParams &p, int32_t *done, int n, int items, int row0,
+__device__ __forceinline__ void publish_items(kp_c &p, int32_t *done, int n, int items, int row0,
                                               int nrows, int layer, int lane) {
     if (n <= 0) return;
     __builtin_amdgcn_s_waitcnt(0);
@@ -910,7 +921,7 @@ __device__ __forceinline__ void publish_items(const KParams &p, int32_t *done, i
 // spreads the waves), claims from it until it is exhausted, and repeats.
 // Routing is a function of the layer's inputs only, so the experts are the
 // owner's.
-__device__ __forceinline__ void steal_upgate(const KParams &p, const SharedState &sh, const u32x4 *act, int layer, int self_k,
+__device__ __forceinline__ void steal_upgate(kp_c &p, const SharedState &sh, const u32x4 *act, int layer, int self_k,
                              int e0, int e1, int lane, int wave) {
     const int n = sh.pool_n;
     const int start = (self_k + 1 + wave) % n;
@@ -936,7 +947,7 @@ __device__ __forceinline__ void steal_upgate(const KParams &p, const SharedState
 // stores of it have completed).  The item that completes the instruction
 // arrives for its blocks on the layer counter and, with the overlap on, adds
 // its rows to the column-chunk counters.
-__device__ __forceinline__ void upgate_item_done(const KParams &p, SharedState &sh, int layer, int k, int lane) {
+__device__ __forceinline__ void upgate_item_done(kp_c &p, SharedState &sh, int layer, int k, int lane) {
     if (lane != 0 || k < 0) return;
     const int r0 = sh.grp_row0[k], n = sh.grp_nrows[k];
     if (atomicAdd(&sh.grp_done[k], 1) + 1 != 2 * n) return;
@@ -956,7 +967,7 @@ __device__ __forceinline__ void upgate_item_done(const KParams &p, SharedState &
 // (kMaxMerge at most) run as one pool of items, so the routing is computed
 // once and no wave waits for another between them.
 template <int kE, bool kSpec>
-__device__ __forceinline__ bool op_rms_router_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
+__device__ __forceinline__ bool op_rms_router_upgate(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                                      const Ctx &c, int32_t *tim, int &consumed) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1270,7 +1281,7 @@ __device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 
 // flight).  The partial sum of each (row, expert, group) goes to LDS, and
 // the row's total is summed over the groups in a fixed order, so the result
 // does not depend on when a group became ready.
-__device__ __forceinline__ bool downproj_overlapped(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool downproj_overlapped(kp_c &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                     int32_t *tim, int layer, int start, int end) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = start * p.down_bs, nrows = (end - start) * p.down_bs;
@@ -1405,7 +1416,7 @@ __device__ __forceinline__ bool downproj_overlapped(const KParams &p, SharedStat
 // kOverlap: the overlapped form is compiled in (the 8-expert MoE-only
 // kernel; in the others its registers would spill).
 template <bool kOverlap>
-__device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
+__device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                    const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int start = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1546,7 +1557,7 @@ __device__ __forceinline__ bool op_expert_downproj(const KParams &p, SharedState
 // ---------------------------------------------------------------------------
 
 template <int kE>
-__device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_predict(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     if (layer < 0 || layer >= p.num_layers) {
@@ -1580,7 +1591,7 @@ __device__ __forceinline__ bool op_predict(const KParams &p, SharedState &sh, u3
 // attention side and LM head: opcodes 1-4 and 7 (python_vm.py:61-222, 321-345)
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ bool need_attention(const KParams &p, const Ctx &c, int op, int layer) {
+__device__ __forceinline__ bool need_attention(kp_c &p, const Ctx &c, int op, int layer) {
     if (p.attn) return true;
     report_error(p, MK_ERR_UNSUPPORTED_OPCODE, c, op, layer, 0, op);
     return false;
@@ -1589,7 +1600,7 @@ __device__ __forceinline__ bool need_attention(const KParams &p, const Ctx &c, i
 // Wait until the counter each of the first n (<= 64) lanes of wave 0 points
 // at reaches `expected`.  Every control value is wave-uniform (ballot,
 // readfirstlane); the result is broadcast to the workgroup like wait_ge's.
-__device__ __forceinline__ bool wait_lanes_ge(const KParams &p, SharedState &sh, const int32_t *mine, int n, int expected,
+__device__ __forceinline__ bool wait_lanes_ge(kp_c &p, SharedState &sh, const int32_t *mine, int n, int expected,
                               const Ctx &c, int opcode, int layer) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
@@ -1625,7 +1636,7 @@ __device__ __forceinline__ bool wait_lanes_ge(const KParams &p, SharedState &sh,
 // act[0 .. H/8) = bf16(w * bf16(h * 1/sqrt(mean(h^2) + eps))) of the current
 // hidden state (python_vm rms_norm, lat/python_vm.py:50-56).  Ends with a
 // workgroup barrier.
-__device__ __forceinline__ void rms_to_lds(const KParams &p, SharedState &sh, u32x4 *act, const uint16_t *w) {
+__device__ __forceinline__ void rms_to_lds(kp_c &p, SharedState &sh, u32x4 *act, const uint16_t *w) {
     const int tid = threadIdx.x, nv = p.H >> 3;
     float ss = 0.f;
     for (int v = tid; v < nv; v += kThreads) ss += sumsq8(ld_dev128(p.hidden, (uint32_t)v * 16u));
@@ -1738,7 +1749,7 @@ __device__ __forceinline__ void matvec_rows_ahead(SharedState &sh, const PairAhe
 
 // ---- opcode 1: Mixtral_QKV  (python_vm.py:61-118) -------------------------
 
-__device__ __forceinline__ bool op_qkv(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_qkv(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                        int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -1880,7 +1891,7 @@ __device__ __forceinline__ void stage_kv(unsigned char *dst, const uint16_t *kba
 // Scores are kept in log2 units (q pre-scaled by attn_scale * log2(e)), so
 // exp(s) = exp2(s2) and the partition's LSE is log2(L) + M.
 template <int GQA>
-__device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh, u32x4 *act, const Ctx &c,
                              int layer, int kv, int nparts, int pidx, int32_t *tim) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int D = a.D, G = D / 8, TPW = 64 / G, CT = kWaves * TPW;
@@ -2119,7 +2130,7 @@ __device__ __forceinline__ bool partial_attn(const KParams &p, attn_c &a, Shared
     return true;
 }
 
-__device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_partial_attn(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                                 int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int kv = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2149,7 +2160,7 @@ __device__ __forceinline__ bool op_partial_attn(const KParams &p, SharedState &s
 // on waves 1.. (wave 0 polls).  A reduction worker otherwise starts its O
 // projection's loads only when the reduction is done, and every other
 // workgroup's opcode 5 then waits for it.
-__device__ __forceinline__ void stage_oproj_rows(const KParams &p, const attn_c &a, SharedState &sh, u32x4 *act,
+__device__ __forceinline__ void stage_oproj_rows(kp_c &p, const attn_c &a, SharedState &sh, u32x4 *act,
                                                  ins_t *nx, int slot, int layer) {
     if (p.late_loads || slot >= p.queue_len) return;
     const int op = __builtin_amdgcn_readfirstlane(nx[0]);
@@ -2172,7 +2183,7 @@ __device__ __forceinline__ void stage_oproj_rows(const KParams &p, const attn_c 
     if (threadIdx.x == 0) sh.ostage_slot = slot;
 }
 
-__device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_attn_reduction(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                                   int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int hs = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2271,7 +2282,7 @@ __device__ __forceinline__ bool op_attn_reduction(const KParams &p, SharedState 
 // item i, matrix j (0 gate, 1 up), chunk c is the 1 KiB at u32x4 index
 // stage_off16 + ((2 i + j) nc + c) 64, lane order.  The loads complete
 // before the workgroup passes its next barrier.
-__device__ __forceinline__ void stage_dense_upgate(const KParams &p, SharedState &sh, u32x4 *act,
+__device__ __forceinline__ void stage_dense_upgate(kp_c &p, SharedState &sh, u32x4 *act,
                                                    ins_t *nx, int slot, int layer) {
     if (p.stage_items <= 0 || slot >= p.queue_len) return;
     const int op = __builtin_amdgcn_readfirstlane(nx[0]);
@@ -2318,7 +2329,7 @@ __device__ __forceinline__ void stage_dense_upgate(const KParams &p, SharedState
 // ends (the O projection's later loads queue behind them).  Opcode 5 uses
 // the rows if its routing picks the predicted expert first.  Wave 0 stages
 // nothing: its thread 0 polls the counter.
-__device__ __forceinline__ void stage_moe_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *nx, int slot,
+__device__ __forceinline__ void stage_moe_upgate(kp_c &p, SharedState &sh, u32x4 *act, ins_t *nx, int slot,
                                                  int layer) {
     if (p.stage_items <= 0 || slot >= p.queue_len) return;
     const int op = __builtin_amdgcn_readfirstlane(nx[0]);
@@ -2356,7 +2367,7 @@ __device__ __forceinline__ void stage_moe_upgate(const KParams &p, SharedState &
     }
 }
 
-__device__ __forceinline__ bool op_oproj(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_oproj(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                          int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2487,7 +2498,7 @@ __device__ __forceinline__ void lm_atomic_pair(uint16_t *logits, int r, float sa
 // The instruction's rows in items of LmRows<NC> rows, the first item of
 // each wave loaded before the wait (the weights do not depend on it).
 template <int NC>
-__device__ __forceinline__ bool lm_head_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool lm_head_rows(kp_c &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                              int32_t *tim, int r0, int nrows, int col0) {
     attn_c &a = attn_of(p);
     const int last = p.num_layers - 1;
@@ -2508,7 +2519,7 @@ __device__ __forceinline__ bool lm_head_rows(const KParams &p, SharedState &sh, 
     return true;
 }
 
-__device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
+__device__ __forceinline__ bool op_lm_head(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                            int32_t *tim) {
     const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2568,7 +2579,7 @@ __device__ __forceinline__ bool op_lm_head(const KParams &p, SharedState &sh, u3
 // silu_out[r] = bf16(bf16(silu(bf16 g)) * bf16 u), g and u the gate and up
 // rows dotted with the normed vector; one arrival per block on [l][4][0].
 // The dense weights are the one-expert case of the opcode-5 item.
-__device__ __forceinline__ bool op_dense_upgate(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
+__device__ __forceinline__ bool op_dense_upgate(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                                 const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int n = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2687,7 +2698,7 @@ __device__ __forceinline__ void load_rows(u32x4 (&w)[NR][NC], const uint16_t *ma
 // chunks (16 loads per lane); each wave's first item is loaded before the
 // wait on opcode 5, since the weights do not depend on it.
 template <int NR, int NC>
-__device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool dense_down_rows(kp_c &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                 int32_t *tim, int layer, int b0, int b1, int red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int R = p.red_cols, col0 = red * R;
@@ -2740,7 +2751,7 @@ __device__ __forceinline__ bool dense_down_rows(const KParams &p, SharedState &s
 // wave (its first kSegChunks chunks) is loaded before the wait, and, when
 // this workgroup's opcode 5 already passed the O-proj wait (the residual
 // rows are final then), so are the first kRowBatch residual rows.
-__device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool dense_down_full(kp_c &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                 int32_t *tim, int layer, int b0, int b1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = b0 * p.down_bs, nrows = (b1 - b0) * p.down_bs;
@@ -2798,7 +2809,7 @@ __device__ __forceinline__ bool dense_down_full(const KParams &p, SharedState &s
     return true;
 }
 
-__device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
+__device__ __forceinline__ bool op_dense_down(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                               const Ctx &c, int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b0 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2826,7 +2837,7 @@ __device__ __forceinline__ bool op_dense_down(const KParams &p, SharedState &sh,
 // [start, end) * lm_head_block_size, stored (not accumulated) with one
 // 32-bit coherent store per row pair.
 template <int NC>
-__device__ __forceinline__ bool dense_lm_head_rows(const KParams &p, SharedState &sh, u32x4 *act, const Ctx &c,
+__device__ __forceinline__ bool dense_lm_head_rows(kp_c &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                    int32_t *tim, int r0, int nrows) {
     attn_c &a = attn_of(p);
     const int last = p.num_layers - 1;
@@ -2848,7 +2859,7 @@ __device__ __forceinline__ bool dense_lm_head_rows(const KParams &p, SharedState
     return true;
 }
 
-__device__ __forceinline__ bool op_dense_lm_head(const KParams &p, SharedState &sh, u32x4 *act, ins_t *ins,
+__device__ __forceinline__ bool op_dense_lm_head(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins,
                                                  const Ctx &c, int32_t *tim) {
     const int b0 = __builtin_amdgcn_readfirstlane(ins[1]);
     const int b1 = __builtin_amdgcn_readfirstlane(ins[2]);
@@ -2916,7 +2927,7 @@ __device__ __forceinline__ void arg_take(ArgBest &a, float v, int idx) {
 // written to p.argmax_out, and with p.next_embed the embedding row of that
 // token copied into hidden.  Replaces the generator's torch.argmax and
 // embedding lookup between launches (megakernels/generators.py:121-145).
-__device__ __forceinline__ void exit_argmax(const KParams &p, SharedState &sh) {
+__device__ __forceinline__ void exit_argmax(kp_c &p, SharedState &sh) {
     attn_c &a = attn_of(p);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int V = a.V, nv = V >> 3;
@@ -2986,7 +2997,7 @@ __device__ __forceinline__ void zero_words(uint32_t *p, size_t n) {
 // work-sharing counters for the next launch, after the decode-driver tail
 // when one was asked for.  Every other workgroup has finished all of its
 // scratch accesses before it increments the counter.
-__device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
+__device__ __forceinline__ void kernel_exit(kp_c &p, SharedState &sh) {
     drain_and_sync();
     if (threadIdx.x == 0) {
         const int prev = __hip_atomic_fetch_add(p.scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3030,7 +3041,8 @@ __device__ __forceinline__ void kernel_exit(const KParams &p, SharedState &sh) {
 }
 
 template <int kE, bool kAttn>
-__global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
+__global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
+    kp_c &p = kparams();
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
     if (threadIdx.x == 0) {
@@ -3089,7 +3101,8 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams p) {
 // Persistent kernel of the dense Llama VM (lat/ opcodes 1-7): the attention
 // side is shared with the Mixtral kernel; opcodes 5-7 are the dense MLP and
 // the LM head.
-__global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams p) {
+__global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams) {
+    kp_c &p = kparams();
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
     if (threadIdx.x == 0) {
