@@ -65,14 +65,6 @@
 #define MK_POOL_GROUP 8
 #endif
 // O-projection rows staged in LDS by a preceding reduction (stage_oproj_rows).
-// Opcode 2: wave priority (s_setprio) of the younger half of the waves
-// while the K/V chunks stream (0: all equal).  Every wave handles the same
-// positions, and with equal priorities the younger wave of each SIMD ended
-// its chunks ~23 % after the older one at config 5 (14.4 vs 11.7 us);
-// priority 1 shortens the partition by ~1.2 us there.
-#ifndef MK_ATTN_PRIO
-#define MK_ATTN_PRIO 1
-#endif
 #ifndef MK_OSTAGE
 #define MK_OSTAGE 1
 #endif
@@ -84,6 +76,11 @@
 #endif
 #ifndef MK_CLAIM_LOOKAHEAD
 #define MK_CLAIM_LOOKAHEAD 1
+#endif
+// Opcode 6: chunks (512 columns) of each wave's first item loaded into
+// registers before the wait for opcode 5.
+#ifndef MK_EARLY_CHUNKS
+#define MK_EARLY_CHUNKS 10
 #endif
 // Opcode-6 cache warming while waiting for opcode 5: items per wave (0 = off).
 #ifndef MK_PF_ROUNDS
@@ -197,6 +194,9 @@ struct KParams {
     uint32_t timeout_ticks;
     int32_t *scratch;
     int32_t work_sharing;
+    // opcode 3 streams its worker's next O-projection rows into LDS while it
+    // waits (stage_oproj_rows): on for the Mixtral VM, off for the dense one
+    int32_t ostage;
     // attention side and LM head (opcodes 1-4, 7): attn == 0 when absent
     int32_t attn;
     uint32_t pos;  // pos_id: changes every decode step, so it stays a kernel argument
@@ -1236,7 +1236,7 @@ __device__ __forceinline__ float dot_row_regs(const RowRegs<N> &r, const u32x4 *
 }
 
 constexpr int kSegChunks = 16;   // max chunks per opcode-6 item (16 KiB per wave)
-constexpr int kEarlyChunks = 8;  // chunks of its first item each wave loads before the opcode-6 wait
+constexpr int kEarlyChunks = MK_EARLY_CHUNKS;  // chunks of its first item each wave loads before the opcode-6 wait
 constexpr int kRowBatch = kRowBatchLds;
 
 struct DownItem {
@@ -1964,12 +1964,6 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
     }
     const bool two = nb >= 2 * kAttnSub;  // two groups resident (uniform)
     const int ngroups = (nch + kAttnSub - 1) / kAttnSub;
-#if MK_ATTN_PRIO
-    // every wave streams the same number of positions, and the SIMD's issue
-    // arbitration favours the older of its two waves: the younger half goes
-    // first while the chunks stream (reset after the loop)
-    if (wave >= kWaves / 2) __builtin_amdgcn_s_setprio(MK_ATTN_PRIO);
-#endif
     for (int g = 0; g < ngroups; ++g) {
         const int cg = g * kAttnSub;
         if (g == 0) {
@@ -2050,9 +2044,6 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
         if (cn < nch) stage_chunks(cn, cn + kAttnSub);
     }
 
-#if MK_ATTN_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
     stamp(tim, MK_TEVENT_AT_GMEM_STORE);  // wave 0's positions done
     // fold the token slots of the wave (lanes with the same dp) to the wave max
 #pragma unroll
@@ -2212,7 +2203,7 @@ __device__ __forceinline__ bool op_attn_reduction(kp_c &p, SharedState &sh, u32x
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 3, layer, hs, n);
         return false;
     }
-    if (MK_OSTAGE) stage_oproj_rows(p, a, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+    if (MK_OSTAGE && p.ostage) stage_oproj_rows(p, a, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!wait_ge(p, sh, bar_at(p, layer, 2) + hs, nparts, c, 3, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
@@ -3608,6 +3599,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
     kp.scratch = st->scratch;
     kp.work_sharing = 0;
+    kp.ostage = 0;
     kp.red_cols = g->matvec_reduction_size;
     kp.late_loads = g->late_loads ? 1 : 0;
     kp.stage_items = (int32_t)stage_items;
@@ -3773,6 +3765,7 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
     kp.scratch = base;
     kp.work_sharing = g->work_sharing ? 1 : 0;
+    kp.ostage = 1;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
     // whole-model launches: the O projection stages up to one predicted
