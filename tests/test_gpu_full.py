@@ -109,3 +109,18 @@ def test_consecutive_steps_reuse_the_cache():
     for p in range(case.pos - 3, case.pos):
         assert max_abs_rel(case.g_gpu.k_cache[:, 0, p], case.g_cpu.k_cache[:, 0, p]) <= TOL
         assert max_abs_rel(case.g_gpu.v_cache[:, 0, p], case.g_cpu.v_cache[:, 0, p]) <= TOL
+
+
+def test_wide_barrier_tensor_leaves_counters_unspread():
+    """A barrier tensor of 2^16 ints or more (here [2, 10, 4096]) turns the
+    XCD-spread layer counters off (their row lookup divides by reciprocals
+    exact below 2^16): every arrival then lands on the tensor itself, and
+    the step still matches the oracle, barriers included."""
+    case = FullCase(TINY, seed=10, prefill=300, steps=2)
+    L, ops, _ = case.g_gpu.barriers.shape
+    for g in (case.g_gpu, case.g_cpu):
+        g.barriers = torch.zeros((L, ops, 4096), dtype=torch.int32, device=g.barriers.device)
+    assert L * ops * 4096 >= 1 << 16
+    for tok in (4, 9):
+        case.step(tok)
+        _check(case, "wide barrier tensor")
