@@ -115,10 +115,13 @@ constexpr int kScratchSlotBase = 16;
 constexpr int kSpread = 8;
 constexpr int kXcds = 8;  // MI355X: workgroup w runs on XCD w % 8 (round-robin dispatch)
 constexpr int kSpreadAlign = 1024;
-// opcodes whose layer counters are spread, per kernel (bit k = opcode k):
-// provisional, set from measurements
-constexpr int32_t kSpreadDenseOps = (1 << 4) | (1 << 5) | (1 << 6);
-constexpr int32_t kSpreadMixtralOps = (1 << 4) | (1 << 5) | (1 << 6);
+// opcodes whose layer counters are spread, per kernel (bit k = opcode k),
+// from same-process A/B runs (MK_SPREAD overrides them): none spread costs
+// config 3 5.4 % and config 4 1.2 %; adding opcode 3's counter (the
+// reductions' arrivals, polled by every O projection) gains config 3 0.5 %
+// and config 4 0.2 %; opcodes 7 and 8 change nothing
+constexpr int32_t kSpreadDenseOps = (1 << 3) | (1 << 4) | (1 << 5) | (1 << 6);
+constexpr int32_t kSpreadMixtralOps = (1 << 3) | (1 << 4) | (1 << 5) | (1 << 6);
 constexpr int32_t kSpreadMoeOps = 0;
 constexpr int kPoolGroup = MK_POOL_GROUP;
 constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) that can be shared
