@@ -69,10 +69,12 @@
 #define MK_OSTAGE 1
 #endif
 // Spin back-off: a waiting workgroup polls its counter every ~64 * N clocks,
-// N growing from 1 to MK_SPIN_SLEEP_MAX, so hundreds of idle workgroups do not
-// keep the counter's memory channel busy while others still stream weights.
+// N doubling from 1 to MK_SPIN_SLEEP_MAX (a launch field), so hundreds of
+// idle workgroups do not keep the memory channels busy while others still
+// stream weights.  Same-process A/B of the cap: 16 beats 4 by 0.4 % at
+// config 3 and 0.2 % at configs 4 and 5; 32 is level with 16, 64 slower.
 #ifndef MK_SPIN_SLEEP_MAX
-#define MK_SPIN_SLEEP_MAX 4
+#define MK_SPIN_SLEEP_MAX 16
 #endif
 #ifndef MK_CLAIM_LOOKAHEAD
 #define MK_CLAIM_LOOKAHEAD 1
@@ -197,6 +199,7 @@ struct KParams {
     uint32_t timeout_ticks;
     int32_t *scratch;
     int32_t work_sharing;
+    int32_t spin_max;  // longest back-off between polls, in s_sleep(1) units
     // opcode 3 streams its worker's next O-projection rows into LDS while it
     // waits (stage_oproj_rows): on for the Mixtral VM, off for the dense one
     int32_t ostage;
@@ -526,7 +529,7 @@ __device__ __forceinline__ bool wait_ge(kp_c &p, SharedState &sh, int32_t *ctr, 
             int nap = 1;
             for (;;) {
                 for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
-                if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
+                if (nap < p.spin_max) nap *= 2;
                 v = counter_value(p, ctr, row);
                 if (v >= expected) break;
                 if (aborted(p)) {
@@ -1336,7 +1339,7 @@ __device__ __forceinline__ bool downproj_overlapped(kp_c &p, SharedState &sh, u3
                     break;
                 }
                 for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
-                if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
+                if (nap < p.spin_max) nap *= 2;
             }
             sh.ready_mask = ok ? (int)ready : -1;
         }
@@ -1626,7 +1629,7 @@ __device__ __forceinline__ bool wait_lanes_ge(kp_c &p, SharedState &sh, const in
                 break;
             }
             for (int i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(1);
-            if (nap < MK_SPIN_SLEEP_MAX) nap *= 2;
+            if (nap < p.spin_max) nap *= 2;
         }
         if (lane == 0) sh.flag = ok;
     }
@@ -3343,6 +3346,14 @@ SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops, int32_t
     return s;
 }
 
+// Longest spin back-off (MK_SPIN_SLEEP_MAX naps; the MK_SPIN_SLEEP
+// environment variable overrides it for measurements).
+int32_t spin_max_naps() {
+    const char *env = std::getenv("MK_SPIN_SLEEP");
+    const long v = env != nullptr ? std::strtol(env, nullptr, 0) : MK_SPIN_SLEEP_MAX;
+    return (int32_t)std::min(64L, std::max(1L, v));
+}
+
 // Opcode-5 items staged ahead in LDS: `n` (what the LDS holds), none with
 // late loads; MK_STAGE_ITEMS=<k> caps it for measurements.
 size_t stage_limit(size_t n, bool late_loads) {
@@ -3602,6 +3613,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
     kp.scratch = st->scratch;
     kp.work_sharing = 0;
+    kp.spin_max = spin_max_naps();
     kp.ostage = 0;
     kp.red_cols = g->matvec_reduction_size;
     kp.late_loads = g->late_loads ? 1 : 0;
@@ -3768,6 +3780,7 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.timeout_ticks = timeout_ticks(g->spin_timeout_us);
     kp.scratch = base;
     kp.work_sharing = g->work_sharing ? 1 : 0;
+    kp.spin_max = spin_max_naps();
     kp.ostage = 1;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
