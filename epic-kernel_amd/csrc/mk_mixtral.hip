@@ -200,6 +200,9 @@ struct KParams {
     int32_t *scratch;
     int32_t work_sharing;
     int32_t spin_max;  // longest back-off between polls, in s_sleep(1) units
+    int32_t tail_items;    // opcode-5 work sharing: items per instruction claimed through its cursor
+    int32_t early_chunks;  // opcode 6: chunks of each wave's first item loaded before the wait (<= kEarlyChunks)
+    int32_t pf_rounds;     // opcode 6: cache-warming rounds while opcode 5 still runs elsewhere
     // opcode 3 streams its worker's next O-projection rows into LDS while it
     // waits (stage_oproj_rows): on for the Mixtral VM, off for the dense one
     int32_t ostage;
@@ -880,7 +883,7 @@ __device__ __forceinline__ void pool_scan_near(kp_c &p, SharedState &sh, int lay
     if (lane == 0) sh.pool_n = __popcll(bal);
 }
 
-__device__ __forceinline__ int tail_items(int items) { return items < MK_TAIL_ITEMS ? items : MK_TAIL_ITEMS; }
+__device__ __forceinline__ int tail_items(kp_c &p, int items) { return items < p.tail_items ? items : p.tail_items; }
 
 __device__ __forceinline__ int32_t *slot_cursor(kp_c &p, int slot) {
     return p.scratch + kScratchSlotBase + 2 * slot;
@@ -934,7 +937,7 @@ __device__ __forceinline__ void steal_upgate(kp_c &p, const SharedState &sh, con
     for (;;) {
         int left = 0;
         if (lane < n && lane != self_k) {
-            const int tail = tail_items(2 * sh.pool_nrows[lane]);
+            const int tail = tail_items(p, 2 * sh.pool_nrows[lane]);
             left = tail - (int)ld_dev32(slot_cursor(p, sh.pool_slot[lane]));
         }
         uint64_t b = __ballot(left > 0);
@@ -942,7 +945,7 @@ __device__ __forceinline__ void steal_upgate(kp_c &p, const SharedState &sh, con
         // first candidate at or after `start`, wrapping around
         const uint64_t hi = b >> start;
         const int v = hi != 0 ? start + (int)__builtin_ctzll(hi) : (int)__builtin_ctzll(b);
-        const int nrows = sh.pool_nrows[v], items = 2 * nrows, tail = tail_items(items);
+        const int nrows = sh.pool_nrows[v], items = 2 * nrows, tail = tail_items(p, items);
         int32_t *cursor = slot_cursor(p, sh.pool_slot[v]);
         const int got = upgate_claimed(p, act, layer, sh.pool_row0[v], nrows, e0, e1, items - tail, tail, cursor, lane);
         publish_items(p, cursor + 1, got, items, sh.pool_row0[v], nrows, layer, lane);
@@ -1129,7 +1132,7 @@ __device__ __forceinline__ bool op_rms_router_upgate(kp_c &p, SharedState &sh, u
         int self_k = 0;
         while (self_k < sh.pool_n - 1 && sh.pool_slot[self_k] != self_slot) ++self_k;
         int32_t *cursor = slot_cursor(p, self_slot);
-        const int items = 2 * nrows, tail = tail_items(items);
+        const int items = 2 * nrows, tail = tail_items(p, items);
         // a wave's first item (item `wave`) may be staged in LDS, as in the
         // static path below
         const bool from_lds = kSpec && kE > 0 && staged > 0 && wave >= 1 && wave <= staged && wave < nrows &&
@@ -1257,16 +1260,16 @@ __device__ __forceinline__ DownItem down_item(int it, int S, int nc) {
     return DownItem{it / (2 * S), (it / S) & 1, c0, c1 - c0};
 }
 
-// Partial dot of one item; with use_pre, its first kEarlyChunks chunks are
-// already in `pre`.
+// Partial dot of one item; its first min(d.n, npre) chunks are already in
+// `pre` (npre = 0: none).
 __device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 *xact, const DownItem &d, int lane,
-                                               bool use_pre, const RowRegs<kEarlyChunks> &pre) {
+                                               int npre, const RowRegs<kEarlyChunks> &pre) {
     const u32x4 *w = reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane;
     const u32x4 *x = xact + d.c0 * 64 + lane;
     float acc = 0.f;
     int done = 0;
-    if (use_pre) {
-        const int n = min(d.n, kEarlyChunks);
+    if (npre > 0) {
+        const int n = min(d.n, npre);
         acc = dot_row_regs<kEarlyChunks>(pre, x, n, acc);
         done = n;
     }
@@ -1446,13 +1449,14 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
         nc <= kGroupChunks * kMaxGroups)
         return downproj_overlapped(p, sh, act, c, tim, layer, start, end);
     const int first_batch = min(nrows, kRowBatch);
-    const bool early = known && wave < first_batch * 2 * S;
+    const int npre_max = min(max(p.early_chunks, 0), kEarlyChunks);
+    const bool early = known && wave < first_batch * 2 * S && npre_max > 0;
     RowRegs<kEarlyChunks> pre;
     if (early) {
         const DownItem d = down_item(wave, S, nc);
         const int e = sh.route_idx[d.slot];
         const uint16_t *row = p.down + ((size_t)(layer * p.E + e) * p.H + row0 + d.row) * (size_t)p.F;
-        load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane, min(d.n, kEarlyChunks));
+        load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane, min(d.n, npre_max));
     }
     // The residual rows this instruction updates: when opcode 5 ran here,
     // the O-projection barrier it waited for has made them final, so they
@@ -1463,19 +1467,18 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     int32_t *ready = bar_at(p, layer, 5);
     const int expected = p.F / p.expert_bs;
-#if MK_PF_ROUNDS > 0
     // Cache warming: if opcode 5 is still running elsewhere, HBM has spare
     // bandwidth, so each wave reads the rows of its next items once more
     // with ordinary (cache-allocating) loads straight into a scratch corner
     // of LDS; after the wait, their regular loads find them in the
     // Infinity Cache.  Workgroups that arrive after the last producer skip
     // it.
-    if (known) {
+    if (known && p.pf_rounds > 0) {
         const bool warm = !counter_reached(p, sh, ready, expected);
         if (warm) {
             __attribute__((address_space(3))) void *sink =
                 (__attribute__((address_space(3))) void *)(act + (lds_prefetch_offset(p) >> 4) + wave * 64);
-            for (int m = 1; m <= MK_PF_ROUNDS; ++m) {
+            for (int m = 1; m <= p.pf_rounds; ++m) {
                 const int it = wave + m * kWaves;
                 if (it >= first_batch * 2 * S) break;
                 const DownItem d = down_item(it, S, nc);
@@ -1488,7 +1491,6 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
             }
         }
     }
-#endif
     if (!wait_ge(p, sh, ready, expected, c, 6, layer)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
 
@@ -1531,8 +1533,8 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
         for (int it = wave; it < items; it = next_local_item(sh, lane)) {
             const DownItem d = down_item(it, S, nc);
             const uint16_t *row = p.down + ((d.slot ? base1 : base0) + row0 + b0 + d.row) * (size_t)p.F;
-            const bool use_pre = early && b0 == 0 && it == wave;
-            const float acc = wave_sum(down_item_dot(row, act + (d.slot ? nv : 0), d, lane, use_pre, pre));
+            const int npre = early && b0 == 0 && it == wave ? npre_max : 0;
+            const float acc = wave_sum(down_item_dot(row, act + (d.slot ? nv : 0), d, lane, npre, pre));
             if (lane == 0) sh.part[(d.row * 2 + d.slot) * kMaxSegments + (it % S)] = acc;
         }
         __syncthreads();
@@ -3346,13 +3348,16 @@ SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops, int32_t
     return s;
 }
 
-// Longest spin back-off (MK_SPIN_SLEEP_MAX naps; the MK_SPIN_SLEEP
-// environment variable overrides it for measurements).
-int32_t spin_max_naps() {
-    const char *env = std::getenv("MK_SPIN_SLEEP");
-    const long v = env != nullptr ? std::strtol(env, nullptr, 0) : MK_SPIN_SLEEP_MAX;
-    return (int32_t)std::min(64L, std::max(1L, v));
+// A tuning value of the launch: `def`, or the environment variable `name`
+// (for measurements), clamped to [lo, hi].
+int32_t env_int(const char *name, long def, long lo, long hi) {
+    const char *env = std::getenv(name);
+    const long v = env != nullptr ? std::strtol(env, nullptr, 0) : def;
+    return (int32_t)std::min(hi, std::max(lo, v));
 }
+
+// Longest spin back-off (MK_SPIN_SLEEP_MAX naps, MK_SPIN_SLEEP overrides it).
+int32_t spin_max_naps() { return env_int("MK_SPIN_SLEEP", MK_SPIN_SLEEP_MAX, 1, 64); }
 
 // Opcode-5 items staged ahead in LDS: `n` (what the LDS holds), none with
 // late loads; MK_STAGE_ITEMS=<k> caps it for measurements.
@@ -3614,6 +3619,9 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.scratch = st->scratch;
     kp.work_sharing = 0;
     kp.spin_max = spin_max_naps();
+    kp.tail_items = env_int("MK_TAIL", MK_TAIL_ITEMS, 1, 1 << 20);
+    kp.early_chunks = env_int("MK_EARLY", MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
+    kp.pf_rounds = env_int("MK_PF", MK_PF_ROUNDS, 0, 4);
     kp.ostage = 0;
     kp.red_cols = g->matvec_reduction_size;
     kp.late_loads = g->late_loads ? 1 : 0;
@@ -3781,6 +3789,9 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.scratch = base;
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.spin_max = spin_max_naps();
+    kp.tail_items = env_int("MK_TAIL", MK_TAIL_ITEMS, 1, 1 << 20);
+    kp.early_chunks = env_int("MK_EARLY", MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
+    kp.pf_rounds = env_int("MK_PF", MK_PF_ROUNDS, 0, 4);
     kp.ostage = 1;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
