@@ -50,8 +50,8 @@ HBM_PEAK_GBS = 8000.0
 # known size: FETCH x 2.0, WRITE x 1.0), measured on commit 7794364: config 2
 # one MoE layer; configs 3/4/5 one decode step at 2050 / 4098 / 16386 cached
 # positions.  The counter runs are summarised under profiles/.
-MEASURED_TRAFFIC_BYTES = {"c2": 708_222_323, "c3": 6_732_320_901, "c4": 26_321_661_941, "c5": 27_934_161_515}
-TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 22dcf85; "
+MEASURED_TRAFFIC_BYTES = {"c2": 708_295_877, "c3": 6_730_852_216, "c4": 26_326_975_555, "c5": 27_932_303_669}
+TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 32d375a; "
                 "configs 3-5 at 2050 / 4098 / 16386 cached positions)")
 
 
