@@ -164,3 +164,38 @@ def test_prediction_agreement_from_the_record():
     assert n == 3  # the layer without a prediction is left out
     assert top1 == pytest.approx(2 / 3) and top2 == pytest.approx(2 / 3)
     assert "top-2 set agreement 66.7%" in format_report(rec)
+
+
+def test_pooled_opcode5_slots_share_the_first_slots_window():
+    """Consecutive opcode-5 instructions of one layer on one worker run as one
+    item pool: the kernel stamps the first slot and copies its start, wait,
+    first-load and done-store times into the pooled slots (each gets its own
+    end).  Every pooled slot's bytes are then counted, spread over the same
+    window, and the binned rate still integrates to the bytes."""
+    W, Q, t0 = 1, 3, 5000
+    ins = np.zeros((W, Q, 32), dtype=np.int32)
+    tim = np.zeros((W, Q, 128), dtype=np.int32)
+    ins[0, 0, :4] = [5, 0, 0, 4]  # 4 blocks of 8 rows
+    ins[0, 1, :4] = [5, 0, 4, 2]  # pooled with slot 0: 2 blocks
+    ins[0, 2, :5] = [6, 0, 0, 32, 0]
+
+    def put(q, slot, us):
+        tim[0, q, slot] = np.uint32((t0 + int(round(us * 100))) & 0xFFFFFFFF).view(np.int32)
+
+    for q, end in ((0, 10.5), (1, 10.6)):
+        for slot, us in ((0, 0.0), (44, 0.5), (45, 1.0), (48, 2.0), (47, 10.0)):
+            put(q, slot, us)
+        put(q, 4, end)
+    for slot, us in ((0, 10.6), (44, 10.7), (45, 11.0), (48, 11.5), (47, 20.0), (4, 20.5)):
+        put(2, slot, us)
+    rec = TimingRecord(tim, ins, H, F, E, expert_proj_block_size=8, down_proj_block_size=16)
+    b0, b1, b6 = rec.streamed_bytes(0, 0), rec.streamed_bytes(0, 1), rec.streamed_bytes(0, 2)
+    assert b0 == 2 * 2 * 32 * H * 2 and b1 == b0 // 2
+    starts, gbs, frac, total = hbm_utilization(rec, bin_us=0.5, peak_gbs=1000.0)
+    assert total == b0 + b1 + b6
+    assert np.sum(gbs) * 0.5 * 1e3 == pytest.approx(total, rel=1e-9)
+    # inside the shared window (2 .. 10 us) both pooled slots stream
+    assert gbs[int(5.0 / 0.5)] == pytest.approx((b0 + b1) / 8.0 / 1e3)
+    bw = barrier_waits(rec)
+    assert bw["by_opcode"][5]["count"] == 2
+    assert bw["by_opcode"][5]["wait_us"] == pytest.approx(2 * 0.5)
