@@ -15,15 +15,24 @@ Also in the same line:
 * ``moe_layer``: one full-size Mixtral MoE layer in isolation (BASELINE
   config 2): 1024 batch-1 tokens per step, each a launch of opcodes 5 and 6,
   its microseconds per launch, HBM roofline fraction of
-  2*(E*H + H + k*3*F*H) bytes, and the skewed-routing variant (+2.0 router
-  bias on experts 0 and 1);
+  2*(E*H + H + k*3*F*H) bytes, the skewed-routing variant (+2.0 router
+  bias on experts 0 and 1) and a same-run correctness gate (8 tokens against
+  the CPU oracle);
+* ``configs``: configs 5 (the same model at 16384 cached positions, with a
+  predictor of router + N(0, sigma) weights, the measured prediction
+  agreement and the predictor on/off A/B) and 3 (Llama-3.2-3B shape, dense
+  VM), timed in the same run, each with its own roofline;
+* ``correctness``: the token and last-layer experts of one whole-model
+  launch over a two-layer slice of the headline model against the CPU
+  oracle's step of the same slice;
 * ``cpu_baseline``: the CPU oracle (a restatement of the reference's
-  python_vm) timed on the host over a bounded slice of the same decode
-  workload and scaled to tokens/s.
+  python_vm; bf16 einsum per block as the reference runs it, and the C +
+  OpenMP leg beside it) timed on the host over a bounded slice of the same
+  decode workload and scaled to tokens/s.
 
 ``python bench.py`` (defaults: 128 timed steps after 2 warmup steps);
 ``--config c2`` / ``c1`` run the MoE layer alone, ``c3`` / ``c5`` the other
-decode configs.
+decode configs alone, ``--c4-only`` the headline alone.
 """
 
 from __future__ import annotations
@@ -47,9 +56,10 @@ METRIC = "batch-1 decode tokens/s, Mixtral-8x7B shape; MoE layer µs; % HBM peak
 HBM_PEAK_GBS = 8000.0
 # HBM bytes moved per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE per
 # dispatch, each scaled by what the same counter reads for a device copy of
-# known size: FETCH x 2.0, WRITE x 1.0), measured on commit 7794364: config 2
-# one MoE layer; configs 3/4/5 one decode step at 2050 / 4098 / 16386 cached
-# positions.  The counter runs are summarised under profiles/.
+# known size: FETCH x 2.0, WRITE x 1.0), measured on the kernel of commit
+# 32d375a: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
+# 4098 / 16386 cached positions.  The counter runs are summarised under
+# profiles/.
 MEASURED_TRAFFIC_BYTES = {"c2": 708_295_877, "c3": 6_730_852_216, "c4": 26_326_975_555, "c5": 27_932_303_669}
 TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 32d375a; "
                 "configs 3-5 at 2050 / 4098 / 16386 cached positions)")
@@ -270,35 +280,71 @@ def decode_bytes_per_token_llama(cfg, seq_len: int) -> int:
     return 2 * (L * (attn + mlp + kv) + V * H + H)
 
 
-def decode_bench(args, config: str, steps: int, warmup: int):
+#: BASELINE config 5: predictor weights = router + N(0, sigma), sigma tuned
+#: for ~80 % top-2 agreement with the true router: a sweep at 16384 cached
+#: positions (``--config c5 --sigma-sweep``, 8 steps x 32 layers each) gave
+#: top-2 set agreement 99.2 / 92.2 / 81.6 / 76.2 / 70.7 / 62.1 % at sigma 0 /
+#: 0.002 / 0.003 / 0.004 / 0.005 / 0.007; the agreement measured in the run
+#: is reported in the bench line
+C5_SIGMA = 0.003
+PREFILL = {"c3": 2048, "c4": 4096, "c5": 16384}
+
+
+def build_decode_model(config: str, positions: int, sigma: float | None, prefill: int | None = None):
+    """Random-init weights resident in HBM (seed 0) and a KV cache pre-filled
+    with N(0, 1) to ``prefill`` positions (default: the config's context),
+    with room for ``positions`` positions in all."""
+    import torch
+
+    prefill = PREFILL[config] if prefill is None else prefill
+    t0 = time.perf_counter()
+    if config == "c3":
+        from megakernels_amd.latency.synthetic import C3, make_synthetic_llama
+
+        cfg = C3
+        print(f"bench: building c3 ({cfg.num_hidden_layers} layers, {prefill} cached positions) on cuda:0",
+              file=sys.stderr, flush=True)
+        model = make_synthetic_llama(cfg, "cuda", 0, kv_positions=positions, prefill=prefill)
+    else:
+        from megakernels_amd.mixtral.synthetic import C4, make_synthetic_mixtral
+
+        cfg = C4
+        print(f"bench: building the Mixtral model ({cfg.num_hidden_layers} layers, {prefill} cached positions) "
+              "on cuda:0", file=sys.stderr, flush=True)
+        model = make_synthetic_mixtral(cfg, "cuda", 0, full=True, kv_positions=positions, prefill=prefill,
+                                       predictor_sigma=sigma)
+    torch.cuda.synchronize()
+    print(f"bench: weights ready in {time.perf_counter() - t0:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB "
+          "allocated", file=sys.stderr, flush=True)
+    return model
+
+
+def decode_bench(args, config: str, steps: int, warmup: int, model=None, sigma: float | None = None,
+                 prefetch_rounds: int | None = None):
     """Whole-model greedy decode through MK_Generator
     (Llama-3.2-3B shape, 2048 cached positions, dense VM) and configs 4 and 5
     (Mixtral-8x7B shape, 4096 / 16384 cached positions).  Random-init weights
     resident in HBM, a KV cache pre-filled with N(0, 1) to the context
-    length, `steps` timed steps after `warmup` untimed ones.  Returns the
-    bench line (a dict) and the model."""
+    length, `steps` timed steps after `warmup` untimed ones.  ``model`` may
+    be given (configs 4 and 5 share one Mixtral model whose cache is filled
+    to 16384 positions; config 4 reads its first 4096); ``sigma``: the
+    predictor weights are the model's router + N(0, sigma) copy, None: the
+    router itself.  Returns the bench line (a dict), the model and the
+    generator."""
     import torch
 
     from megakernels_amd.mixtral.generate import MK_Generator
-    from megakernels_amd.mixtral.synthetic import C4, make_synthetic_mixtral
 
     llama = config == "c3"
     if llama:
-        from megakernels_amd.latency.synthetic import C3, make_synthetic_llama
-
-        cfg, prefill = C3, 2048
+        from megakernels_amd.latency.synthetic import C3 as cfg
     else:
-        cfg, prefill = C4, (4096 if config == "c4" else 16384)
-    print(f"bench: building {config} ({cfg.num_hidden_layers} layers, {prefill} cached positions) on cuda:0",
-          file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    if llama:
-        model = make_synthetic_llama(cfg, "cuda", 0, kv_positions=prefill + steps + warmup + 1, prefill=prefill)
-    else:
-        model = make_synthetic_mixtral(cfg, "cuda", 0, full=True, kv_positions=prefill + steps + warmup + 1,
-                                       prefill=prefill, predictor_sigma=args.predict_sigma)
-    torch.cuda.synchronize()
-    build_s = time.perf_counter() - t0
+        from megakernels_amd.mixtral.synthetic import C4 as cfg
+    prefill = PREFILL[config]
+    if model is None:
+        model = build_decode_model(config, prefill + steps + warmup + 1, sigma)
+    if not llama and sigma is not None and model.stacked_params.predictor_weight is None:
+        raise ValueError("a predictor sigma needs a model built with predictor weights")
     gkw = {"attention_partitions": args.partitions}
     if args.qkv_block:
         gkw["qkv_block_size"] = args.qkv_block
@@ -310,8 +356,9 @@ def decode_bench(args, config: str, steps: int, warmup: int):
                              device_argmax=not args.host_argmax, reset_next=not args.no_reset,
                              late_loads=args.late_loads, xcd_rows=tuple(int(x) for x in args.xcd_rows.split(",") if x),
                              **({} if llama else {"work_sharing": not args.no_work_sharing}))
-    print(f"bench: weights ready in {build_s:.0f} s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated; "
-          f"{len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
+    if not llama and sigma is None:
+        gen.schedule.globs.predictor_weights = None  # opcode 8 predicts with the router itself
+    print(f"bench: {config}: {len(gen.schedule.dag_nodes)} instructions per step", file=sys.stderr, flush=True)
     tokens, secs = gen.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=warmup)
     gpu_s = gen.last_gpu_seconds
     import mk_mixtral
@@ -331,7 +378,8 @@ def decode_bench(args, config: str, steps: int, warmup: int):
         rec = TimingRecord.from_globals(g0)
         save_record(args.trace, rec)
         print(format_report(rec), file=sys.stderr, flush=True)
-    ab = prefetch_ab(args, gen, model, prefill, steps, llama, gkw) if args.prefetch_ab else None
+    rounds = args.prefetch_ab if prefetch_rounds is None else prefetch_rounds
+    ab = prefetch_ab(args, gen, model, prefill, steps, llama, gkw, rounds, sigma) if rounds else None
     ms = secs / steps * 1e3
     nbytes = (decode_bytes_per_token_llama if llama else decode_bytes_per_token)(cfg, prefill + steps // 2)
     kernel_s = gpu_s / steps
@@ -363,7 +411,7 @@ def decode_bench(args, config: str, steps: int, warmup: int):
             "workers": g.sm_count(),
             "attention_partitions": int(max(i.num_partials for i in gen.schedule.get_linear_instructions()
                                             if i.opcode() == 2)),
-            "predictor_sigma": args.predict_sigma,
+            "predictor_sigma": None if llama else sigma,
             "predictor": None if llama else not args.no_predict,
             "assignment": args.assign,
             "qkv_block_size": g.qkv_block_size,
@@ -399,7 +447,70 @@ def decode_bench(args, config: str, steps: int, warmup: int):
     return out, model, gen
 
 
-def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: dict):
+def prediction_agreement(gen, prefill: int, steps: int = 8) -> dict:
+    """Opcode 8's predicted expert pair against the pair opcode 5 selects, in
+    every layer of ``steps`` decode steps (timing record on, after the timed
+    run; each step's input is the previous step's token): the fraction of
+    layers whose predicted top-1 is the selected top-1, whose predicted pair
+    is the selected pair as a set (top-2 agreement), and the mean fraction
+    of the two selected experts that were predicted."""
+    import torch
+
+    from megakernels_amd.trace import T_PREDICTION, TimingRecord
+
+    g = gen.schedule.globs
+    gen.launch_kwargs["record_timings"] = True
+    tok = torch.ones((1, 1), dtype=torch.long, device=g.hidden_states.device)
+    pairs = []
+    try:
+        for i in range(steps):
+            g.timings.zero_()
+            tok = gen.run(tok, pos_id=prefill + i).reshape(1, 1)
+            torch.cuda.synchronize()
+            rec = TimingRecord.from_globals(g)
+            ins, tim = rec.instructions, rec.timings
+            seen = set()
+            for w, q in zip(*((ins[:, :, 0] == 5).nonzero())):
+                layer = int(ins[w, q, 1])
+                v = int(tim[w, q, T_PREDICTION]) & 0xFFFFFFFF
+                if layer in seen or v == 0 or v & 0xFF == 0xFF:
+                    continue
+                seen.add(layer)
+                pairs.append((v & 0xFF, (v >> 8) & 0xFF, (v >> 16) & 0xFF, (v >> 24) & 0xFF))
+    finally:
+        gen.launch_kwargs.pop("record_timings", None)
+        gen.fill()
+        gen._clean = False
+    n = len(pairs)
+    if n == 0:
+        return {"layers": 0}
+    return {
+        "layers": n,
+        "steps": steps,
+        "top1": sum(p0 == s0 for p0, _, s0, _ in pairs) / n,
+        "top2_set": sum({p0, p1} == {s0, s1} for p0, p1, s0, s1 in pairs) / n,
+        "expert_overlap": sum(len({p0, p1} & {s0, s1}) for p0, p1, s0, s1 in pairs) / (2 * n),
+        "definition": "per layer of each step: predicted top-1 == selected top-1 (top1); predicted pair == "
+                      "selected pair as a set (top2_set, the agreement the predictor sigma is tuned for); "
+                      "mean fraction of the selected pair that was predicted (expert_overlap)",
+    }
+
+
+def set_predictor_sigma(model, sigma: float, seed: int = 7) -> None:
+    """predictor weights <- bf16(router + N(0, sigma)), in place (the
+    tensor the launches read)."""
+    import torch
+
+    sp = model.stacked_params
+    g = torch.Generator(device=sp.router_weight.device)
+    g.manual_seed(seed)
+    noise = torch.empty(sp.router_weight.shape, dtype=torch.float32, device=sp.router_weight.device)
+    noise.normal_(0.0, sigma, generator=g)
+    sp.predictor_weight.copy_((sp.router_weight.float() + noise).to(sp.predictor_weight.dtype))
+
+
+def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: dict, rounds: int,
+                sigma: float | None = None):
     """Prefetch on vs off in the same process, alternating for
     ``args.prefetch_ab`` rounds of ``steps`` decode steps each (medians of
     HIP-event tokens/s): "on" is the default launch; "late_loads" waits for
@@ -426,8 +537,11 @@ def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: di
     if not llama:
         variants["no_predict"] = MK_Generator.build(model, prefill, mode=args.assign, globals_kwargs=gkw,
                                                     dag_kwargs={"predict": False}, **base)
+        if sigma is None:
+            for v in variants.values():
+                v.schedule.globs.predictor_weights = None
     rates = {k: [] for k in variants}
-    for r in range(args.prefetch_ab):
+    for r in range(rounds):
         for name, g in variants.items():
             g.timed_generate(first_token=1, prompt_len=prefill, ntok=steps, warmup=1)
             rates[name].append(steps / g.last_gpu_seconds)
@@ -438,7 +552,7 @@ def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: di
     mk_mixtral.raise_if_failed("cuda")
     med = {k: statistics.median(v) for k, v in rates.items()}
     out = {
-        "rounds": args.prefetch_ab,
+        "rounds": rounds,
         "steps_per_round": steps,
         "tokens_per_s": {k: round(v, 2) for k, v in med.items()},
         "all": {k: [round(x, 2) for x in v] for k, v in rates.items()},
@@ -455,13 +569,19 @@ def prefetch_ab(args, gen, model, prefill: int, steps: int, llama: bool, gkw: di
     return out
 
 
-def cpu_baseline_decode(model, prefill: int, seconds: float, threads: int, sm_count: int, layers: int = 2):
-    """The CPU oracle (restated python_vm: C + OpenMP matvecs, torch CPU
-    attention) on a bounded slice of the config-4 decode step: the first
-    ``layers`` layers of the same model with the LM head, at the same cached
-    context, stepped until ``seconds`` have passed.  The per-layer time and
-    the LM head's time are measured separately and scaled to a whole step
-    of all L layers: tokens/s = 1 / (L * t_layer + t_lm_head)."""
+def cpu_baseline_decode(model, prefill: int, seconds: float, threads: int, sm_count: int, layers: int = 2,
+                        backend: str = "torch", cpu=None):
+    """The CPU oracle (a restatement of the reference's python_vm) on a
+    bounded slice of the config-4 decode step: the first ``layers`` layers
+    of the same model with the LM head, at the same cached context, stepped
+    until ``seconds`` have passed.  ``backend`` "torch": the reference's own
+    CPU arithmetic, bf16 einsum per 16-row block and torch CPU attention
+    (lat/python_vm.py:29-56); "c": the oracle's C + OpenMP matvecs.  The
+    per-layer time and the LM head's time are measured separately and scaled
+    to a whole step of all L layers: tokens/s = 1 / (L * t_layer +
+    t_lm_head).  Also returns the state after the first step (token 1 at
+    position ``prefill``): its token and last-layer experts, for the
+    same-run correctness gate."""
     import torch
 
     from megakernels_amd.mixtral.scheduler import make_dag, make_globals
@@ -472,45 +592,169 @@ def cpu_baseline_decode(model, prefill: int, seconds: float, threads: int, sm_co
     oracle.set_num_threads(threads)
     torch.set_num_threads(threads)
     L = model.config.num_hidden_layers
-    cpu = slice_layers(model, layers, "cpu")
+    if cpu is None:
+        cpu = slice_layers(model, layers, "cpu")
     g = make_globals(cpu, seq_len=prefill, sm_count=sm_count)
+    g.predictor_weights = None
     g.pos_id = prefill
     nodes, end = make_dag(g)
     linear = Schedule(g, nodes, end).get_linear_instructions()
     t_layers = t_head = 0.0
     steps = 0
-    t0 = time.perf_counter()
-    while steps == 0 or time.perf_counter() - t0 < seconds:
-        g.hidden_states.copy_(cpu.embed_tokens[1 + steps])
-        g.barriers.zero_()
-        g.logits.zero_()
-        for ins in linear:
-            t1 = time.perf_counter()
-            oracle.INSTRUCTION_TO_SOLVER[type(ins)](g, ins)
-            dt = time.perf_counter() - t1
-            if ins.opcode() == 7:
-                t_head += dt
-            else:
-                t_layers += dt
-        steps += 1
-    elapsed = time.perf_counter() - t0
+    first = None
+    oracle.set_backend(backend)
+    try:
+        t0 = time.perf_counter()
+        while steps == 0 or time.perf_counter() - t0 < seconds:
+            g.hidden_states.copy_(cpu.embed_tokens[1 + steps])
+            g.barriers.zero_()
+            g.logits.zero_()
+            for ins in linear:
+                t1 = time.perf_counter()
+                oracle.INSTRUCTION_TO_SOLVER[type(ins)](g, ins)
+                dt = time.perf_counter() - t1
+                if ins.opcode() == 7:
+                    t_head += dt
+                else:
+                    t_layers += dt
+            if steps == 0:
+                rl = oracle.router_logits(g.router_weights[layers - 1].contiguous(), g.router_normed_hidden)
+                top = torch.sort(rl, descending=True).values
+                lg = torch.sort(g.logits.float(), descending=True).values
+                first = {"token": int(torch.argmax(g.logits)), "experts": g.selected_expert_indices.tolist(),
+                         "router_gaps": [float(top[0] - top[1]), float(top[1] - top[2])],
+                         "logit_gap": float(lg[0] - lg[1]), "hidden": g.hidden_states.clone()}
+            steps += 1
+        elapsed = time.perf_counter() - t0
+    finally:
+        oracle.set_backend("c")
     per_layer = t_layers / steps / layers
     head = t_head / steps
     token_s = L * per_layer + head
-    return {
+    how = ("bf16 einsum per 16-row block as the reference's python_vm (lat/python_vm.py:29-56), torch CPU "
+           "attention" if backend == "torch" else "C+OpenMP matvecs, torch CPU attention")
+    out = {
         "value": 1.0 / token_s,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
         "sample": f"{steps} decode steps of layers 0-{layers - 1} of the same config-4 model with its LM head, "
                   f"{prefill} cached positions, through the oracle python_vm restatement ({len(linear)} "
-                  f"instructions per step, C+OpenMP matvecs and torch CPU attention), {elapsed:.1f} s; "
+                  f"instructions per step, {how}), {elapsed:.1f} s; "
                   f"per token = {L} x {per_layer * 1e3:.1f} ms per layer + {head * 1e3:.1f} ms LM head",
+        "backend": backend,
         "ms_per_layer": per_layer * 1e3,
         "ms_lm_head": head * 1e3,
+        "torch_threads": torch.get_num_threads(),
         "cpu_model": cpu_model_name(),
         "os_cpu_count": os.cpu_count(),
     }
+    return out, first
+
+
+#: router-logit / LM-head logit gap below which the gate accepts a
+#: different order (after two layers the residual differs from the
+#: oracle's by up to max-abs-rel ~1e-2)
+GATE_MARGIN = 0.05
+
+
+def decode_gate(model, prefill: int, oracle_first: dict, sm_count: int, layers: int = 2) -> dict:
+    """Same-run correctness gate of the headline: one launch of the
+    whole-model kernel over the same ``layers``-layer slice of the model
+    (its LM head included) that the CPU oracle stepped, from the same token
+    and position; the token (argmax inside the launch) and the last layer's
+    expert pair against the oracle's, exact unless the oracle's own gap is
+    below GATE_MARGIN, and the residual within max-abs-rel 2e-2."""
+    import torch
+
+    import mk_mixtral
+    from megakernels_amd.mixtral.mk import interpret_with_mk
+    from megakernels_amd.mixtral.scheduler import make_dag, make_globals
+    from megakernels_amd.mixtral.synthetic import slice_layers
+    from megakernels_amd.scheduler import Schedule, assign_to_sms, tensorize_instructions
+
+    sl = slice_layers(model, layers, "cuda")
+    g = make_globals(sl, seq_len=prefill, sm_count=sm_count)
+    g.predictor_weights = None
+    g.pos_id = prefill
+    nodes, end = make_dag(g)
+    tensorize_instructions(g, assign_to_sms("rr", schedule=Schedule(g, nodes, end)))
+    g.hidden_states.copy_(sl.embed_tokens[1])
+    g.barriers.zero_()
+    g.logits.zero_()
+    tok = torch.full((), -1, dtype=torch.long, device="cuda")
+    interpret_with_mk(g, mk_mixtral.mk_mixtral, argmax_out=tok, debug_sync=True, work_sharing=True)
+    torch.cuda.synchronize()
+    gtok, gexp = int(tok), g.selected_expert_indices.cpu().tolist()
+    ref = oracle_first
+    gap01, gap12 = ref["router_gaps"]
+    if gap12 < GATE_MARGIN:
+        experts_ok = gexp[0] == ref["experts"][0] or gap01 < GATE_MARGIN
+    elif gap01 < GATE_MARGIN:
+        experts_ok = sorted(gexp) == sorted(ref["experts"])
+    else:
+        experts_ok = gexp == ref["experts"]
+    token_ok = gtok == ref["token"] or ref["logit_gap"] < GATE_MARGIN
+    h, r = g.hidden_states.cpu().float(), ref["hidden"].float()
+    err = float((h - r).abs().max() / r.abs().max())
+    del sl, g
+    torch.cuda.empty_cache()
+    return {
+        "what": f"one whole-model launch over layers 0-{layers - 1} of the bench model with its LM head (token 1 "
+                f"at position {prefill}) against the CPU oracle's first step of the same slice",
+        "token": gtok, "oracle_token": ref["token"], "oracle_logit_gap": ref["logit_gap"],
+        "last_layer_experts": gexp, "oracle_experts": ref["experts"], "oracle_router_gaps": ref["router_gaps"],
+        "hidden_max_abs_rel": err,
+        "passed": bool(token_ok and experts_ok and err <= 2e-2),
+    }
+
+
+def c2_gate(bench, n: int = 8) -> dict:
+    """Same-run correctness gate of the config-2 layer: ``n`` of its tokens
+    launched one by one and run through the CPU oracle (C backend) from the
+    same residuals; expert pairs exact, hidden and SiLU within max-abs-rel
+    2e-2 (drawn residuals: where the oracle's 2nd and 3rd router logits are
+    within 1e-3, the order of the pair is not held)."""
+    import torch
+
+    from megakernels_amd.mixtral.scheduler import make_globals, prefill_oproj_barrier
+    from megakernels_amd.mixtral.synthetic import to_device
+    from oracle import python_vm as oracle
+
+    cpu_model = to_device(bench.model, "cpu")
+    g = make_globals(cpu_model, sm_count=bench.globs.sm_count(),
+                     expert_proj_block_size=bench.globs.expert_proj_block_size,
+                     down_proj_block_size=bench.globs.down_proj_block_size)
+    linear = bench.linear_instructions()
+    residuals = bench.residuals.cpu()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(bench.dev).cuda_stream)
+    equal = ties = 0
+    worst = 0.0
+    for t in range(n):
+        bench.work[t].copy_(bench.residuals[t])
+        bench.bars[t].copy_(bench.bars_init[t])
+        bench._launch(t, stream)
+        torch.cuda.synchronize()
+        gi = bench.globs.selected_expert_indices.cpu()
+        silu = bench.globs.expert_silu_out.cpu()
+        gh = bench.work[t].cpu()
+        g.barriers.zero_()
+        prefill_oproj_barrier(g)
+        g.hidden_states.copy_(residuals[t])
+        oracle.interpret_with_pyvm(g, linear)
+        ri = g.selected_expert_indices
+        rl = torch.sort(oracle.router_logits(g.router_weights[0].contiguous(), g.router_normed_hidden),
+                        descending=True).values
+        if torch.equal(gi, ri):
+            equal += 1
+        elif float(rl[1] - rl[2]) < 1e-3 or float(rl[0] - rl[1]) < 1e-3:
+            ties += 1
+        idx = ri.long()
+        for y, r in ((gh, g.hidden_states), (silu[idx], g.expert_silu_out[idx])):
+            worst = max(worst, float((y.float() - r.float()).abs().max() / r.float().abs().max()))
+    bench.check_status()
+    return {"tokens": n, "experts_equal": equal, "near_ties": ties, "max_abs_rel_hidden_silu": worst,
+            "passed": equal + ties == n and worst <= 2e-2}
 
 
 def layer_bench(args, config: str, steps: int, warmup: int):
@@ -638,6 +882,95 @@ def cpu_baseline_layer(bench, seconds: float, threads: int):
     }
 
 
+def compact(line: dict) -> dict:
+    """The figures of a decode bench line that another config's line carries."""
+    keep = ("value", "unit", "steps", "warmup", "ms_per_step", "ms_per_step_hip_events", "roofline", "prefetch_ab",
+            "prediction_agreement", "tokens_tail")
+    out = {k: line[k] for k in keep if k in line}
+    out["config"] = line["config"]
+    return out
+
+
+def headline(args, threads: int, warmup: int) -> dict:
+    """The default run.  Config 4 is the headline (``value``); configs 2, 5
+    and 3 are timed in the same process and carried as extra keys, each with
+    its own roofline:
+
+    1. config 2 (one MoE layer per launch) on the fresh device, with its
+       same-run correctness gate;
+    2. one Mixtral model whose KV cache is filled to 16384 positions:
+       config 4 decodes at 4096 (predictor = the router), then the CPU
+       oracle on a two-layer slice of it (torch-bf16 and C legs) and the
+       same-run correctness gate, then config 5 at 16384 with predictor
+       weights = router + N(0, C5_SIGMA), its predictor A/B and the
+       measured prediction agreement;
+    3. config 3 (Llama-3.2-3B shape, dense VM) on its own model."""
+    import torch
+
+    layer_fig = None
+    if not args.no_layer:
+        layer_fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
+        layer_fig["correctness"] = c2_gate(bench)
+        print(f"bench: c2 gate {layer_fig['correctness']}", file=sys.stderr, flush=True)
+        del bench
+        torch.cuda.empty_cache()
+    steps = args.steps or args.decode_steps or 128
+    c5_steps = args.extra_steps or 128
+    sigma = C5_SIGMA if args.predict_sigma is None else args.predict_sigma
+    positions = PREFILL["c5"] + max(steps + warmup, c5_steps + 2, 8) + 16
+    model = build_decode_model("c4", positions, sigma, prefill=PREFILL["c5"])
+    out, model, gen = decode_bench(args, "c4", steps, warmup, model=model, sigma=None)
+    sm = gen.schedule.globs.sm_count()
+    del gen
+    if not args.no_cpu:
+        print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s per leg)", file=sys.stderr,
+              flush=True)
+        cpu_t, first = cpu_baseline_decode(model, PREFILL["c4"], args.cpu_seconds, threads, sm, backend="torch")
+        cpu_c, _ = cpu_baseline_decode(model, PREFILL["c4"], args.cpu_seconds, threads, sm, backend="c")
+        cpu_t["c_openmp_leg"] = cpu_c
+        out["cpu_baseline"] = cpu_t
+        out["correctness"] = decode_gate(model, PREFILL["c4"], first, sm)
+        print(f"bench: c4 gate passed={out['correctness']['passed']}", file=sys.stderr, flush=True)
+    extra = {}
+    if not args.no_extra:
+        c5, model, gen = decode_bench(args, "c5", c5_steps, 2, model=model, sigma=sigma)
+        c5["prediction_agreement"] = prediction_agreement(gen, PREFILL["c5"])
+        print(f"bench: c5 prediction agreement {c5['prediction_agreement']}", file=sys.stderr, flush=True)
+        extra["c5"] = compact(c5)
+        del gen
+    del model
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        c3_steps = args.extra_steps or 256
+        c3, m3, gen = decode_bench(args, "c3", c3_steps, 2)
+        extra["c3"] = compact(c3)
+        del m3, gen
+        torch.cuda.empty_cache()
+    if layer_fig is not None:
+        out["moe_layer"] = layer_fig
+    if extra:
+        out["configs"] = extra
+    return out
+
+
+def sigma_sweep(args, model, sigmas) -> list:
+    """Prediction agreement of the config-5 decode (16384 cached positions)
+    for each predictor noise level: predictor weights <- router + N(0,
+    sigma), then the agreement over 8 recorded steps of all layers."""
+    from megakernels_amd.mixtral.generate import MK_Generator
+
+    gen = MK_Generator.build(model, PREFILL["c5"], mode=args.assign,
+                             globals_kwargs={"attention_partitions": args.partitions})
+    out = []
+    for sg in sigmas:
+        set_predictor_sigma(model, sg)
+        a = prediction_agreement(gen, PREFILL["c5"])
+        a["sigma"] = sg
+        print(f"bench: sigma {sg}: {a}", file=sys.stderr, flush=True)
+        out.append(a)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -656,8 +989,14 @@ def main():
     ap.add_argument("--layer-steps", type=int, default=10,
                     help="c4: timed steps (of --tokens launches) of the config-2 layer figures")
     ap.add_argument("--no-layer", action="store_true", help="c4: leave out the config-2 layer figures")
-    ap.add_argument("--layer-after", action="store_true",
-                    help="c4: time the config-2 layer after the decode run instead of before it")
+    ap.add_argument("--c4-only", action="store_true",
+                    help="c4: the config-4 decode alone (with its CPU baseline and gate), not the default line "
+                         "that also times configs 2, 5 and 3")
+    ap.add_argument("--no-extra", action="store_true", help="default run: leave out configs 5 and 3")
+    ap.add_argument("--extra-steps", type=int, default=0,
+                    help="default run: timed steps of configs 5 and 3 (default: 128 and 256, as BASELINE states)")
+    ap.add_argument("--sigma-sweep", default="", metavar="S1,S2,...",
+                    help="c5: only measure the prediction agreement for each predictor noise level and exit")
     ap.add_argument("--assign", default="rr", choices=["rr", "zz", "wave", "dag"],
                     help="c3/c4/c5: instruction-to-worker assignment of the whole-model schedule")
     ap.add_argument("--qkv-block", type=int, default=0,
@@ -671,7 +1010,8 @@ def main():
     ap.add_argument("--no-predict", action="store_true",
                     help="c4/c5: leave out opcode 8 (expert prediction) and the early expert loads that use it")
     ap.add_argument("--predict-sigma", type=float, default=None,
-                    help="c4/c5: predictor weights = router + N(0, sigma) (default: the router itself)")
+                    help="c5: predictor weights = router + N(0, sigma) (default: C5_SIGMA; config 4 predicts "
+                         "with the router itself)")
     ap.add_argument("--late-loads", action="store_true",
                     help="c3/c4/c5: prefetch off -- every instruction waits for its inputs before any of its "
                          "loads, nothing is staged ahead in LDS")
@@ -734,28 +1074,30 @@ def main():
     threads = args.cpu_threads or os.cpu_count()
     warmup = max(1, args.warmup)
     if args.config in ("c3", "c4", "c5"):
+        if args.config == "c4" and not args.c4_only:
+            print(json.dumps(headline(args, threads, warmup)), flush=True)
+            return
         steps = args.steps or args.decode_steps or (256 if args.config == "c3" else 128)
-        layer_fig = None
-        if args.config == "c4" and not args.no_layer and not args.layer_after:
-            # the config-2 layer first, on a device that has not yet held the
-            # 94 GB model
-            layer_fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
-            del bench
-            torch.cuda.empty_cache()
-        out, model, gen = decode_bench(args, args.config, steps, warmup)
+        sigma = args.predict_sigma
+        if sigma is None and args.config == "c5":
+            sigma = C5_SIGMA
+        model = None
+        if args.config != "c3":
+            positions = PREFILL[args.config] + steps + warmup + 16
+            model = build_decode_model(args.config, positions, sigma)
+            if args.sigma_sweep:
+                sweep = sigma_sweep(args, model, [float(x) for x in args.sigma_sweep.split(",")])
+                print(json.dumps({"sigma_sweep": sweep}), flush=True)
+                return
+        out, model, gen = decode_bench(args, args.config, steps, warmup, model=model, sigma=sigma)
+        if args.config == "c5":
+            out["prediction_agreement"] = prediction_agreement(gen, PREFILL["c5"])
         if args.config == "c4" and not args.no_cpu:
-            print(f"bench: CPU oracle baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)", file=sys.stderr,
-                  flush=True)
-            out["cpu_baseline"] = cpu_baseline_decode(model, out["config"]["prefill"], args.cpu_seconds, threads,
-                                                      gen.schedule.globs.sm_count())
+            out["cpu_baseline"], first = cpu_baseline_decode(model, PREFILL["c4"], args.cpu_seconds, threads,
+                                                             gen.schedule.globs.sm_count())
+            out["correctness"] = decode_gate(model, PREFILL["c4"], first, gen.schedule.globs.sm_count())
         del model, gen
         torch.cuda.empty_cache()
-        if args.config == "c4" and not args.no_layer and args.layer_after:
-            layer_fig, bench, _ = layer_bench(args, "c2", args.layer_steps, 2)
-            del bench
-            torch.cuda.empty_cache()
-        if layer_fig is not None:
-            out["moe_layer"] = layer_fig
         print(json.dumps(out), flush=True)
         return
 

@@ -39,6 +39,9 @@
 
 #include <math.h>
 #include <algorithm>
+#include <cctype>
+#include <cerrno>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -3318,8 +3321,14 @@ int launch_persistent(const void *fn, DeviceState *st, int64_t workers, size_t l
     if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel");
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "hipGetLastError");
-    st->launched = true;
-    st->last_stream = stream;
+    // a no-allocation launch is ordered by its caller and is not what a later
+    // launch orders itself after: its stream may be capturing a graph, and
+    // an event recorded there for a launch on another stream would pull
+    // that stream into the capture
+    if (may_allocate) {
+        st->launched = true;
+        st->last_stream = stream;
+    }
     return MK_OK;
 }
 
@@ -3333,12 +3342,60 @@ struct SpreadLayout {
     size_t offset, rows, stride, end;
 };
 
+// Launch-time tuning overrides, for measurements: MK_SPREAD, MK_SPIN_SLEEP,
+// MK_TAIL, MK_EARLY, MK_PF and MK_STAGE_ITEMS.  The environment is read once
+// per process, at the first launch (mk_mixtral_reload_overrides reads it
+// again).  A value that is not a whole number is ignored with a warning on
+// stderr, and each override in effect is reported there when it is read, so
+// a stray variable in a serving process shows instead of silently changing
+// the scheduling.
+enum { kOvSpread, kOvSpinSleep, kOvTail, kOvEarly, kOvPf, kOvStageItems, kOvCount };
+struct TuningOverride {
+    const char *name;
+    bool set;
+    long value;
+};
+TuningOverride g_overrides[kOvCount] = {{"MK_SPREAD", false, 0}, {"MK_SPIN_SLEEP", false, 0},
+                                        {"MK_TAIL", false, 0},   {"MK_EARLY", false, 0},
+                                        {"MK_PF", false, 0},     {"MK_STAGE_ITEMS", false, 0}};
+std::mutex g_overrides_mutex;
+bool g_overrides_read = false;
+
+void read_overrides_locked() {
+    for (TuningOverride &o : g_overrides) {
+        o.set = false;
+        const char *env = std::getenv(o.name);
+        if (env == nullptr || *env == '\0') continue;
+        char *end = nullptr;
+        errno = 0;
+        const long v = std::strtol(env, &end, 0);
+        while (end != nullptr && std::isspace((unsigned char)*end)) ++end;
+        if (errno != 0 || end == env || end == nullptr || *end != '\0') {
+            std::fprintf(stderr, "mk_mixtral: ignoring %s=\"%s\" (not a whole number)\n", o.name, env);
+            continue;
+        }
+        o.set = true;
+        o.value = v;
+        std::fprintf(stderr, "mk_mixtral: measurement override %s=%ld in effect\n", o.name, v);
+    }
+    g_overrides_read = true;
+}
+
+// The override `k`, or nothing: `*value` is set only when one is in effect.
+bool tuning_override(int k, long *value) {
+    std::lock_guard<std::mutex> lock(g_overrides_mutex);
+    if (!g_overrides_read) read_overrides_locked();
+    if (!g_overrides[k].set) return false;
+    *value = g_overrides[k].value;
+    return true;
+}
+
 // `ops`: bit k set spreads the counters of opcode k (the default is the
 // caller's); MK_SPREAD=<bits> overrides it for measurements.
 SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops, int32_t ops) {
     SpreadLayout s{};
-    const char *env = std::getenv("MK_SPREAD");
-    if (env != nullptr) ops = (int32_t)std::strtol(env, nullptr, 0);
+    long v = 0;
+    if (tuning_override(kOvSpread, &v)) ops = (int32_t)v;
     s.ops = ops;
     s.on = ops != 0;
     s.rows = (size_t)layers * (size_t)bar_ops;
@@ -3348,22 +3405,22 @@ SpreadLayout spread_layout(size_t used, int64_t layers, int64_t bar_ops, int32_t
     return s;
 }
 
-// A tuning value of the launch: `def`, or the environment variable `name`
-// (for measurements), clamped to [lo, hi].
-int32_t env_int(const char *name, long def, long lo, long hi) {
-    const char *env = std::getenv(name);
-    const long v = env != nullptr ? std::strtol(env, nullptr, 0) : def;
+// A tuning value of the launch: `def`, or the override `k` (for
+// measurements), clamped to [lo, hi].
+int32_t tuning_value(int k, long def, long lo, long hi) {
+    long v = def;
+    (void)tuning_override(k, &v);
     return (int32_t)std::min(hi, std::max(lo, v));
 }
 
 // Longest spin back-off (MK_SPIN_SLEEP_MAX naps, MK_SPIN_SLEEP overrides it).
-int32_t spin_max_naps() { return env_int("MK_SPIN_SLEEP", MK_SPIN_SLEEP_MAX, 1, 64); }
+int32_t spin_max_naps() { return tuning_value(kOvSpinSleep, MK_SPIN_SLEEP_MAX, 1, 64); }
 
 // Opcode-5 items staged ahead in LDS: `n` (what the LDS holds), none with
 // late loads; MK_STAGE_ITEMS=<k> caps it for measurements.
 size_t stage_limit(size_t n, bool late_loads) {
-    const char *env = std::getenv("MK_STAGE_ITEMS");
-    if (env != nullptr) n = std::min(n, (size_t)std::max(0L, std::strtol(env, nullptr, 0)));
+    long v = 0;
+    if (tuning_override(kOvStageItems, &v)) n = std::min(n, (size_t)std::max(0L, v));
     return late_loads ? 0 : n;
 }
 
@@ -3619,9 +3676,9 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.scratch = st->scratch;
     kp.work_sharing = 0;
     kp.spin_max = spin_max_naps();
-    kp.tail_items = env_int("MK_TAIL", MK_TAIL_ITEMS, 1, 1 << 20);
-    kp.early_chunks = env_int("MK_EARLY", MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
-    kp.pf_rounds = env_int("MK_PF", MK_PF_ROUNDS, 0, 4);
+    kp.tail_items = tuning_value(kOvTail, MK_TAIL_ITEMS, 1, 1 << 20);
+    kp.early_chunks = tuning_value(kOvEarly, MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
+    kp.pf_rounds = tuning_value(kOvPf, MK_PF_ROUNDS, 0, 4);
     kp.ostage = 0;
     kp.red_cols = g->matvec_reduction_size;
     kp.late_loads = g->late_loads ? 1 : 0;
@@ -3668,6 +3725,11 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
 }
 
 int mk_mixtral_abi_version(void) { return MK_MIXTRAL_ABI_VERSION; }
+
+void mk_mixtral_reload_overrides(void) {
+    std::lock_guard<std::mutex> lock(g_overrides_mutex);
+    read_overrides_locked();
+}
 
 int mk_mixtral_last_hip_error(void) { return g_last_hip_error; }
 
@@ -3789,9 +3851,9 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.scratch = base;
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.spin_max = spin_max_naps();
-    kp.tail_items = env_int("MK_TAIL", MK_TAIL_ITEMS, 1, 1 << 20);
-    kp.early_chunks = env_int("MK_EARLY", MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
-    kp.pf_rounds = env_int("MK_PF", MK_PF_ROUNDS, 0, 4);
+    kp.tail_items = tuning_value(kOvTail, MK_TAIL_ITEMS, 1, 1 << 20);
+    kp.early_chunks = tuning_value(kOvEarly, MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
+    kp.pf_rounds = tuning_value(kOvPf, MK_PF_ROUNDS, 0, 4);
     kp.ostage = 1;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;

@@ -142,6 +142,9 @@ class Instruction:
 #: partials a reduction instruction lists explicitly: its 32-word instruction
 #: holds 7 other words
 MAX_LISTED_PARTIALS = 25
+#: partials one reduction instruction can combine at all: the kernel reads a
+#: head's partition LSEs with one wave, one lane each
+MAX_REDUCED_PARTIALS = 64
 
 
 def serialize_reduction(ins) -> list[int]:
@@ -151,8 +154,14 @@ def serialize_reduction(ins) -> list[int]:
     instruction (MAX_LISTED_PARTIALS entries).  A longer list that is the
     range ``0 .. n - 1`` is written as ``-n`` with no entries (no reference
     counterpart: the MI355X partition policy splits the cache over up to 64
-    partitions per KV head); any other longer list is an error."""
+    partitions per KV head); any other longer list is an error, and so is a
+    list of more than MAX_REDUCED_PARTIALS, which the kernel cannot reduce
+    (the reference policy allows ``min(W, 160) // kv_heads`` partitions: 80
+    with two KV heads)."""
     n = len(ins.reduction_list)
+    if n > MAX_REDUCED_PARTIALS:
+        raise ValueError(f"{type(ins).__name__}: {n} partials to reduce; one instruction combines at most "
+                         f"{MAX_REDUCED_PARTIALS} (use fewer attention partitions)")
     if n > MAX_LISTED_PARTIALS and list(ins.reduction_list) == list(range(n)):
         out = 0 if ins.output_partial_idx is None else int(ins.output_partial_idx)
         return [int(ins.opcode()), int(ins.layer_idx), int(ins.head_start_idx), int(ins.num_partials),

@@ -197,6 +197,7 @@ EXPORTED_SYMBOLS = (
     "mk_mixtral_last_hip_error",
     "mk_mixtral_last_error_site",
     "mk_mixtral_abi_version",
+    "mk_mixtral_reload_overrides",
 )
 
 _lib = None
@@ -231,6 +232,8 @@ def load_library():
     lib.mk_mixtral_last_hip_error.restype = ctypes.c_int
     lib.mk_mixtral_last_error_site.restype = ctypes.c_char_p
     lib.mk_mixtral_abi_version.restype = ctypes.c_int
+    lib.mk_mixtral_reload_overrides.argtypes = []
+    lib.mk_mixtral_reload_overrides.restype = None
     if lib.mk_mixtral_abi_version() != ABI_VERSION:
         raise MKError(1, f"{path} has ABI {lib.mk_mixtral_abi_version()}, expected {ABI_VERSION}")
     _lib = lib

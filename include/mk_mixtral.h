@@ -276,7 +276,10 @@ int mk_mixtral_launch(const mk_mixtral_globals *g, void *stream);
  *     zeroed when its last workgroup exits.  Calls that overlap on one GPU
  *     race: unlike mk_mixtral_launch, this entry point records and waits on
  *     no event, so the caller orders it after launches on other streams
- *     (one stream for all launches does that). */
+ *     (one stream for all launches does that).  Nor does a later
+ *     mk_mixtral_launch order itself after a no-allocation launch (its
+ *     stream may be capturing a graph): it follows the previous
+ *     mk_mixtral_launch only, and the caller orders the two kinds. */
 int mk_mixtral_launch_noalloc(const mk_mixtral_globals *g, void *stream);
 
 /* Copy the library-owned status words of `device` into out[16] after a
@@ -291,6 +294,16 @@ int mk_mixtral_clear_status(int device);
  * co-resident for this kernel.  Counterpart of get_sm_count
  * (megakernels/utils.py:133-135). */
 int mk_mixtral_query_device(int device, int32_t *num_cus, int32_t *max_workers);
+
+/* Read the launch-time tuning overrides (MK_SPREAD, MK_SPIN_SLEEP, MK_TAIL,
+ * MK_EARLY, MK_PF, MK_STAGE_ITEMS) from the environment again.  No
+ * reference counterpart: these are measurement settings of this build.  The
+ * library reads them once per process, at its first launch; a value that is
+ * not a whole number is ignored with a warning, and each override in effect
+ * is reported on stderr when read.  Shared by mk_mixtral_launch,
+ * mk_mixtral_launch_noalloc and mk_llama_launch; call it while no launch is
+ * being made from another thread. */
+void mk_mixtral_reload_overrides(void);
 
 const char *mk_mixtral_error_string(int code);
 /* hipError_t and the name of the HIP call behind the last MK_ERR_HIP on the

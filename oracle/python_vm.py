@@ -119,6 +119,39 @@ def _p(t: torch.Tensor):
 
 
 # ---------------------------------------------------------------------------
+# arithmetic backends
+# ---------------------------------------------------------------------------
+#
+# "c" (the default): the bf16 matvecs and the RMS norm in moe_oracle.c (C +
+# OpenMP), with the rounding points of torch's bf16 CPU ops.
+# "torch": the reference's own CPU arithmetic, call for call -- einsum of a
+# bf16 block of 16 rows with a bf16 vector (lat/python_vm.py:29-47, called
+# per block by the solvers of mkm/python_vm.py:258-275 and :296-310), the
+# RMS norm as torch expressions (lat/python_vm.py:50-56).  Same rounding
+# points, torch's own summation order; used as the CPU baseline that runs
+# the way the reference's python_vm does.
+
+_BACKEND = "c"
+#: rows per einsum of the torch backend (the reference's expert block size)
+TORCH_BLOCK_ROWS = 16
+
+
+def set_backend(name: str) -> None:
+    global _BACKEND
+    if name not in ("c", "torch"):
+        raise ValueError(f"unknown oracle backend {name!r}")
+    _BACKEND = name
+
+
+def get_backend() -> str:
+    return _BACKEND
+
+
+def _einsum_rows(mat: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
+    return torch.einsum("oi,i->o", mat, vec)
+
+
+# ---------------------------------------------------------------------------
 # arithmetic helpers
 # ---------------------------------------------------------------------------
 
@@ -126,6 +159,10 @@ def rms_norm(inp: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tenso
     """bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))) -- lat/python_vm.py:50-56."""
     _cpu(inp, torch.bfloat16)
     _cpu(weight, torch.bfloat16)
+    if _BACKEND == "torch":
+        x = inp.to(torch.float32)
+        x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+        return weight * x.to(inp.dtype)
     out = torch.empty_like(inp)
     lib().orc_rms_norm(_p(inp), _p(weight), inp.numel(), float(eps), _p(out))
     return out
@@ -136,6 +173,9 @@ def router_logits(router_w: torch.Tensor, normed: torch.Tensor, bias: torch.Tens
     _cpu(router_w, torch.bfloat16)
     _cpu(normed, torch.bfloat16)
     E, H = router_w.shape
+    if _BACKEND == "torch":
+        out = router_w.float() @ normed.float()
+        return out if bias is None else out + bias.float()
     out = torch.empty(E, dtype=torch.float32)
     b = None if bias is None else _p(_cpu(bias.float().contiguous()))
     lib().orc_router_logits(_p(router_w), _p(normed), E, H, b, _p(out))
@@ -151,6 +191,8 @@ def matvec(mat: torch.Tensor, vec: torch.Tensor, row0: int = 0, nrows: int | Non
     nrows = mat.shape[0] - row0 if nrows is None else nrows
     if not 0 <= row0 <= row0 + nrows <= mat.shape[0] or vec.numel() != mat.shape[1]:
         raise ValueError("matvec: rows or vector length out of range")
+    if _BACKEND == "torch":
+        return _einsum_rows(mat[row0:row0 + nrows], vec)
     out = torch.empty(nrows, dtype=torch.bfloat16)
     lib().orc_matvec(_p(mat), mat.stride(0), _p(vec), mat.shape[1], row0, nrows, _p(out))
     return out
@@ -160,6 +202,14 @@ def upgate_silu(gate: torch.Tensor, up: torch.Tensor, normed: torch.Tensor, row0
     """bf16(bf16(silu(bf16(g))) * bf16(u)) for rows of one expert -- mkm/python_vm.py:258-275."""
     for t in (gate, up, normed):
         _cpu(t, torch.bfloat16)
+    if _BACKEND == "torch":
+        parts = []
+        for r in range(row0, row0 + nrows, TORCH_BLOCK_ROWS):
+            r1 = min(r + TORCH_BLOCK_ROWS, row0 + nrows)
+            g = _einsum_rows(gate[r:r1], normed)
+            u = _einsum_rows(up[r:r1], normed)
+            parts.append((torch.nn.functional.silu(g) * u).to(torch.bfloat16))
+        return torch.cat(parts) if parts else torch.empty(0, dtype=torch.bfloat16)
     out = torch.empty(nrows, dtype=torch.bfloat16)
     lib().orc_upgate_silu(_p(gate), _p(up), _p(normed), gate.shape[1], row0, nrows, _p(out))
     return out
@@ -170,6 +220,12 @@ def down_accumulate(down: torch.Tensor, act: torch.Tensor, row0: int, nrows: int
     """hidden[r] = bf16(hidden[r] + bf16(score * bf16(down[r] @ act))) -- mkm/python_vm.py:300-310."""
     for t in (down, act, hidden):
         _cpu(t, torch.bfloat16)
+    if _BACKEND == "torch":
+        s = torch.tensor(score, dtype=torch.float32)  # the 0-dim fp32 score of mkm/python_vm.py:297
+        for r in range(row0, row0 + nrows, TORCH_BLOCK_ROWS):
+            r1 = min(r + TORCH_BLOCK_ROWS, row0 + nrows)
+            hidden[r:r1] += (s * _einsum_rows(down[r:r1], act)).to(hidden.dtype)
+        return
     lib().orc_down_accumulate(_p(down), _p(act), down.shape[1], row0, nrows, float(score), _p(hidden))
 
 

@@ -142,6 +142,27 @@ def test_version_and_error_strings(lib):
     assert b"unknown" in lib.mk_mixtral_error_string(12345)
 
 
+def test_tuning_overrides_are_reported_and_malformed_ones_ignored(lib, capfd, monkeypatch):
+    """The measurement overrides are read from the environment once per
+    process (mk_mixtral_reload_overrides reads them again): each one in
+    effect is reported on stderr, a value that is not a whole number is
+    ignored with a warning, and nothing is reported without them."""
+    for name in ("MK_SPREAD", "MK_SPIN_SLEEP", "MK_TAIL", "MK_EARLY", "MK_PF", "MK_STAGE_ITEMS"):
+        monkeypatch.delenv(name, raising=False)
+    monkeypatch.setenv("MK_TAIL", "8")
+    monkeypatch.setenv("MK_PF", " 0x2 ")
+    monkeypatch.setenv("MK_EARLY", "4x")
+    lib.mk_mixtral_reload_overrides()
+    err = capfd.readouterr().err
+    assert "measurement override MK_TAIL=8 in effect" in err
+    assert "measurement override MK_PF=2 in effect" in err
+    assert 'ignoring MK_EARLY="4x"' in err and "MK_EARLY=4" not in err
+    for name in ("MK_TAIL", "MK_PF", "MK_EARLY"):
+        monkeypatch.delenv(name)
+    lib.mk_mixtral_reload_overrides()
+    assert "mk_mixtral:" not in capfd.readouterr().err
+
+
 def test_launch_validation_needs_no_gpu(lib):
     # a null struct and a struct of the wrong ABI are rejected before any HIP call
     assert lib.mk_mixtral_launch(None, None) == 1

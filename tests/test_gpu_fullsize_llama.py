@@ -85,3 +85,38 @@ def test_fullsize_dense_decode_properties(model):
     assert int(tok3) == int(tok)
     assert torch.equal(g.logits.cpu(), logits), "prefetch off changed the logits"
     assert torch.equal(g.hidden_states.cpu(), hidden), "prefetch off changed the residual"
+
+
+LAST_LAYER_STAGES = {
+    (None, "qkv"): ("k_new", "v_new", "q"),
+    ("qkv", "reduction"): ("attn_out",),
+    ("reduction", "oproj"): ("hidden",),
+    ("oproj", "upgate"): ("silu",),
+    ("upgate", "downproj"): ("hidden",),
+}
+
+
+@pytest.mark.parametrize("stage", list(LAST_LAYER_STAGES), ids=lambda s: f"{s[0] or 'start'}-{s[1]}")
+def test_last_layer_stage_against_oracle(model, stage):
+    """Layer 27 of the 28-layer 3B-shaped model against the dense oracle on a
+    one-layer copy of its weights and cache, stage by stage from the
+    oracle's state: outputs at least 99 % bit-identical, the barrier row
+    equal."""
+    from layer_harness import LayerCase
+    from moe_harness import MIN_EXACT
+
+    last = model.config.num_hidden_layers - 1
+    case = LayerCase(model, last, PREFILL)
+    g = torch.Generator().manual_seed(77)
+    for _ in range(2):
+        x = torch.randn(case.g_cpu.hidden_size, generator=g).to(torch.bfloat16)
+        case.run(*stage, x)
+        err, agr = case.errors(), case.agreement()
+        tag = f"layer {last} {stage}"
+        print(f"[{tag}] " + " ".join(f"{k} {v:.1e}" for k, v in err.items()), flush=True)
+        print(f"[{tag}] ulp/exact " + " ".join(f"{k} {u}/{e:.4f}" for k, (u, e) in agr.items()), flush=True)
+        for k, v in err.items():
+            assert v <= 2e-2, f"{tag} {k}: max-abs-rel {v:.3e}"
+        for k in LAST_LAYER_STAGES[stage]:
+            assert agr[k][1] >= MIN_EXACT, f"{tag} {k}: {agr[k][1]:.4f} bit-identical"
+        assert case.barriers_equal(), f"{tag}: barrier tensor differs"

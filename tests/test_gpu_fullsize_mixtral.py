@@ -117,3 +117,87 @@ def test_fullsize_decode_properties(model, pos):
         assert torch.equal(first[k], shared[k]), f"work sharing changed {k}"
     print(f"[fullsize pos {pos}] token {int(tok)}, last layer experts {first['sel'].tolist()} "
           f"(predicted {first['pred'].tolist()})", flush=True)
+
+
+# ---------------------------------------------------------------------------
+# the last layer of the full tensors against the oracle, stage by stage
+# ---------------------------------------------------------------------------
+
+#: (after, through) -> outputs held to 99 % bit-identical (and, second, to
+#: one ulp), as the layer-0 stage tests of test_gpu_configs.py hold them
+LAST_LAYER_STAGES = {
+    (None, "qkv"): (("k_new", "v_new", "q"), ()),          # with opcode 8 (the prediction)
+    ("qkv", "reduction"): (("attn_out",), ()),
+    ("reduction", "oproj"): (("hidden",), ()),
+    ("oproj", "rms_router_upgate"): (("normed", "silu"), ("normed",)),
+    ("rms_router_upgate", "downproj"): (("hidden",), ()),
+}
+
+#: predictor-logit gap below which opcode 8's pair may legitimately come out
+#: in another order (fp32 summation order); the drawn residuals are
+#: redrawn until the gaps exceed it
+PREDICT_MARGIN = 1e-3
+
+
+def _stage_id(stage):
+    return f"{stage[0] or 'start'}-{stage[1]}"
+
+
+def _residual(case, seed: int) -> torch.Tensor:
+    """A residual N(0, 1), redrawn until the oracle's predictor logits of the
+    case's layer separate its top three by PREDICT_MARGIN."""
+    g = torch.Generator().manual_seed(seed)
+    for _ in range(64):
+        x = torch.randn(case.g_cpu.hidden_size, generator=g).to(torch.bfloat16)
+        case.residual = x
+        gap01, gap12 = case.predictor_margins()
+        if min(gap01, gap12) > PREDICT_MARGIN:
+            return x
+    raise AssertionError("no residual with separated predictor logits")
+
+
+@pytest.mark.parametrize("pos", [4096, PREFILL_C5], ids=["c4", "c5"])
+@pytest.mark.parametrize("stage", list(LAST_LAYER_STAGES), ids=_stage_id)
+def test_last_layer_stage_against_oracle(model, pos, stage):
+    """Layer 31 of the 32-layer model (its gate/up/down rows 29-31 GiB into
+    the expert tensors, its K/V rows past 2 GiB into the caches) against the
+    oracle on a one-layer copy of the same weights and cache: each stage
+    from the oracle's state, its outputs at the rounding-point bar, the
+    barrier row equal, the selected experts exact and, in the first stage,
+    opcode 8's predicted pair equal to the oracle's (predictor weights =
+    router + N(0, 0.007))."""
+    from layer_harness import LayerCase
+    from moe_harness import MAX_ULP, MIN_EXACT
+
+    last = model.config.num_hidden_layers - 1
+    case = LayerCase(model, last, pos)
+    after, through = stage
+    for seed in (1, 2):
+        x = _residual(case, 1000 * pos + seed)
+        case.run(after, through, x)
+        err, agr = case.errors(), case.agreement()
+        tag = f"layer {last} pos {pos} {_stage_id(stage)}"
+        print(f"[{tag}] " + " ".join(f"{k} {v:.1e}" for k, v in err.items()), flush=True)
+        print(f"[{tag}] ulp/exact " + " ".join(f"{k} {u}/{e:.4f}" for k, (u, e) in agr.items()), flush=True)
+        keys, one_ulp = LAST_LAYER_STAGES[stage]
+        for k, v in err.items():
+            assert v <= 2e-2, f"{tag} {k}: max-abs-rel {v:.3e}"
+        for k in keys:
+            ulp, exact = agr[k]
+            if k in one_ulp:
+                assert ulp <= MAX_ULP, f"{tag} {k}: {ulp} ulps"
+            assert exact >= MIN_EXACT, f"{tag} {k}: {exact:.4f} bit-identical"
+        assert case.barriers_equal(), f"{tag}: barrier tensor differs"
+        gi = case.g_gpu.selected_expert_indices.cpu().tolist()
+        ri = case.g_cpu.selected_expert_indices.tolist()
+        if through in ("rms_router_upgate", "downproj"):
+            gap01, gap12 = case.router_margins()
+            if min(gap01, gap12) > PREDICT_MARGIN:  # else fp32 summation order may swap a near-tie
+                assert gi == ri, f"{tag}: experts {gi} != oracle {ri}"
+            else:
+                print(f"[{tag}] router near-tie {gap01:.2e} {gap12:.2e}: experts {gi} oracle {ri}", flush=True)
+        if after is None:
+            gp = case.g_gpu.predicted_expert_indices.cpu().tolist()
+            rp = case.g_cpu.predicted_expert_indices.tolist()
+            print(f"[{tag}] predicted {gp} oracle {rp} margins {case.predictor_margins()}", flush=True)
+            assert gp == rp, f"{tag}: predicted {gp} != oracle {rp}"

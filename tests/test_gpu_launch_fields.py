@@ -20,7 +20,9 @@ launch: token (argmax inside the launch), logits, residual, the appended K
 and V rows, the selected experts, and the barrier tensor.  Each variant
 runs on a two-layer slice at the exact config-4 (Mixtral-8x7B, 4096 cached
 positions) or config-3 (Llama-3.2-3B, 2048 cached) shape, so every path
-runs at its real trip counts.  The environment is read at each launch.
+runs at its real trip counts.  The library reads the environment once per
+process; the test has it read again (``mk_mixtral_reload_overrides``) after
+each change.
 """
 
 import pytest
@@ -34,15 +36,19 @@ pytestmark = pytest.mark.gpu
 
 FIELDS = ("MK_SPIN_SLEEP", "MK_TAIL", "MK_EARLY", "MK_PF", "MK_SPREAD", "MK_STAGE_ITEMS")
 
-#: (variable, value): both ends of each clamp range that the kernel accepts,
-#: spreading off and on for opcode 5 alone, staging off and partial
+#: (variable, value): both ends of each clamp range that the kernel accepts
+#: (MK_TAIL 4096: every item of an instruction goes through the cursor, no
+#: own-item loop and no staged rows used), a middle value, spreading off and
+#: on for opcode 5 alone, staging off and partial, and a malformed value,
+#: which is ignored
 VARIANTS = [
     ("MK_SPIN_SLEEP", "1"), ("MK_SPIN_SLEEP", "64"),
-    ("MK_TAIL", "1"), ("MK_TAIL", "64"),
-    ("MK_EARLY", "0"), ("MK_EARLY", "4"),
-    ("MK_PF", "0"), ("MK_PF", "2"),
+    ("MK_TAIL", "1"), ("MK_TAIL", "64"), ("MK_TAIL", "4096"),
+    ("MK_EARLY", "0"), ("MK_EARLY", "4"), ("MK_EARLY", "10"),
+    ("MK_PF", "0"), ("MK_PF", "2"), ("MK_PF", "4"),
     ("MK_SPREAD", "0"), ("MK_SPREAD", "0x20"),
     ("MK_STAGE_ITEMS", "0"), ("MK_STAGE_ITEMS", "3"),
+    ("MK_TAIL", "8x"),
 ]
 
 MIXTRAL_POS = 4096
@@ -80,15 +86,24 @@ def _launch(gen, lib, token: int, pos: int, **kw):
     return state
 
 
+def _reload():
+    import mk_mixtral
+
+    mk_mixtral.load_library().mk_mixtral_reload_overrides()
+
+
 def _sweep(gen, lib, token, pos, monkeypatch, **kw):
+    _reload()
     base = _launch(gen, lib, token, pos, **kw)
     assert bool(torch.isfinite(base["logits"].float()).all()) and bool(base["logits"].float().abs().max() > 0)
     assert int(base["token"]) == int(torch.argmax(base["logits"]))
     for name, value in VARIANTS:
         print(f"[launch fields {lib}] {name}={value}", flush=True)
         monkeypatch.setenv(name, value)
+        _reload()
         got = _launch(gen, lib, token, pos, **kw)
         monkeypatch.delenv(name)
+        _reload()
         for k in base:
             assert torch.equal(base[k], got[k]), f"{name}={value} changed {k}"
 

@@ -70,6 +70,24 @@ def test_serialize_words():
     assert Mixtral_AttnReduction(0, 0, 25, True, list(range(25))).serialize()[5:7] == [25, 0]
     with pytest.raises(ValueError):
         serialize_and_pad(Mixtral_AttnReduction(0, 0, 40, True, list(range(1, 41))))
+    # the kernel combines at most 64 partials (one lane each): 64 is written,
+    # 65 fails while the schedule is built, not on the device
+    assert serialize_and_pad(Mixtral_AttnReduction(0, 0, 64, True, list(range(64))))[5] == -64
+    with pytest.raises(ValueError, match="at most 64"):
+        serialize_and_pad(Mixtral_AttnReduction(0, 0, 80, True, list(range(80))))
+
+
+def test_reference_policy_with_two_kv_heads_fails_when_tensorized():
+    """The reference's partition policy allows min(W, 160) // kv_heads
+    partitions (80 with two KV heads at 160+ workers); the schedule that
+    needs an 80-partial reduction is refused when its instructions are
+    written, before any launch."""
+    from megakernels_amd.mixtral.scheduler import pick_num_attention_partitions
+
+    n = pick_num_attention_partitions(32768, 0, 2, 256, "reference")
+    assert n == 80
+    with pytest.raises(ValueError, match="at most 64"):
+        serialize_and_pad(Mixtral_AttnReduction(0, 0, n, True, list(range(n))))
 
 
 def test_round_robin_and_zig_zag():

@@ -305,3 +305,33 @@ def test_matvec_column_block_against_fp64():
     assert float(diff.max()) <= float(ref.float().abs().max()) * 2 ** -7
     # the wrong block (a transposed or shifted read) does not match
     assert not torch.equal(got, oracle.matvec(w[:, :2048], v, 8, 40))
+
+
+@pytest.mark.parametrize("H,F", [(1024, 3584), (512, 1024)])
+def test_torch_backend_moe_layer_bit_level(H, F):
+    """One MoE layer through the oracle's torch backend (the reference's
+    own CPU arithmetic: bf16 einsum per 16-row block) and its C backend from
+    the same input: same experts and scores, normed hidden, SiLU rows and
+    hidden within one bf16 ulp and at least 99 % bit-identical."""
+    from moe_harness import bf16_agreement
+
+    g = torch.Generator().manual_seed(H + F)
+    E = 8
+    x = torch.randn(H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    R = (0.02 * torch.randn(E, H, generator=g)).to(torch.bfloat16)
+    G = (0.02 * torch.randn(E, F, H, generator=g)).to(torch.bfloat16)
+    U = (0.02 * torch.randn(E, F, H, generator=g)).to(torch.bfloat16)
+    D = (0.02 * torch.randn(E, H, F, generator=g)).to(torch.bfloat16)
+    res = {}
+    try:
+        for backend in ("c", "torch"):
+            oracle.set_backend(backend)
+            res[backend] = oracle.moe_layer(x, w, R, G, U, D, 1e-5)
+    finally:
+        oracle.set_backend("c")
+    (hc, ic, sc, nc, uc, _), (ht, it, st, nt, ut, _) = res["c"], res["torch"]
+    assert torch.equal(ic, it) and torch.equal(sc, st)
+    for a, b in ((hc, ht), (nc, nt), (uc, ut)):
+        ulp, exact = bf16_agreement(b, a)
+        assert ulp <= 1 and exact >= 0.99

@@ -198,3 +198,44 @@ def test_oproj_and_lm_head_closed_forms():
     full = g.lm_head_weights.double() @ normed.double()
     err = (g.logits.double() - full).abs().max() / full.abs().max()
     assert float(err) < 1e-2
+
+
+@pytest.mark.parametrize("config,layers", [(SMALL, 2), (TINY, 2)])
+def test_torch_backend_matches_c_backend(config, layers):
+    """The oracle's torch backend (the reference's own CPU arithmetic: bf16
+    einsum per 16-row block, the RMS norm as torch expressions) against the
+    C backend on one whole decode step: same experts and barrier tensor,
+    every output within max-abs-rel 2e-2 (after two layers, attention over
+    the cache spreads the one-ulp differences of the two summation orders),
+    and both held to the fp64 textbook step.  The single MoE layer is held
+    to the bit-level bar in test_oracle.py."""
+    from moe_harness import max_abs_rel
+
+    out = {}
+    try:
+        for backend in ("c", "torch"):
+            oracle.set_backend(backend)
+            model, g = _full(config, layers)
+            _oracle_step(model, g, 7, g.pos_id)
+            pos = g.pos_id
+            out[backend] = {"hidden": g.hidden_states.clone(), "k": g.k_cache[:, 0, pos].clone(),
+                            "v": g.v_cache[:, 0, pos].clone(), "q": g.post_ln_rope_q.clone(),
+                            "attn": g.attn_out.clone(), "silu": g.expert_silu_out.clone(),
+                            "normed": g.router_normed_hidden.clone(), "logits": g.logits.clone(),
+                            "sel": g.selected_expert_indices.clone(), "bar": g.barriers.clone()}
+            h64, _, _, _ = _textbook_step(model, 7, pos)
+            assert float((g.hidden_states.double() - h64).abs().max() / h64.abs().max()) < 3e-2, backend
+    finally:
+        oracle.set_backend("c")
+    c, t = out["c"], out["torch"]
+    assert torch.equal(c["sel"], t["sel"]) and torch.equal(c["bar"], t["bar"])
+    for k in ("hidden", "k", "v", "q", "attn", "silu", "normed", "logits"):
+        if not c[k].any():
+            continue
+        assert max_abs_rel(t[k], c[k]) <= 2e-2, k
+
+
+def test_torch_backend_is_selected_explicitly():
+    assert oracle.get_backend() == "c"
+    with pytest.raises(ValueError):
+        oracle.set_backend("numpy")
