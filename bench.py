@@ -932,6 +932,7 @@ def headline(args, threads: int, warmup: int) -> dict:
         out["correctness"] = decode_gate(model, PREFILL["c4"], first, sm)
         print(f"bench: c4 gate passed={out['correctness']['passed']}", file=sys.stderr, flush=True)
     extra = {}
+    args.trace = ""  # a --trace record is of the headline (config 4) step
     if not args.no_extra:
         c5, model, gen = decode_bench(args, "c5", c5_steps, 2, model=model, sigma=sigma)
         c5["prediction_agreement"] = prediction_agreement(gen, PREFILL["c5"])
