@@ -82,10 +82,10 @@
 #ifndef MK_CLAIM_LOOKAHEAD
 #define MK_CLAIM_LOOKAHEAD 1
 #endif
-// Opcode 6: chunks (512 columns) of each wave's first item loaded into
-// registers before the wait for opcode 5.
-#ifndef MK_EARLY_CHUNKS
-#define MK_EARLY_CHUNKS 10
+// Opcode 6: each wave loads its two first items (both register sets)
+// before the wait for opcode 5 (0 = after it).
+#ifndef MK_EARLY_LOADS
+#define MK_EARLY_LOADS 1
 #endif
 // Opcode-6 cache warming while waiting for opcode 5: items per wave (0 = off).
 #ifndef MK_PF_ROUNDS
@@ -133,7 +133,8 @@ constexpr int kMaxPoolIns = 64;  // opcode-5 instructions per (layer, group) tha
 constexpr int kPoolWindow = 8;  // queue slots per group member pool_scan_near looks at
 static_assert(kMaxPoolIns <= 64, "one lane per group instruction");
 constexpr int kRowBatchLds = 64;  // rows per opcode-6 batch (partial sums in LDS)
-constexpr int kMaxSegments = 4;   // column segments per opcode-6 row (F <= 4 * 16 * 512)
+constexpr int kMaxSegments = 10;  // column segments per opcode-6 row (F <= 10 * 7 * 512)
+constexpr int kMaxIntermediate = 32768;  // largest intermediate size the launch accepts
 constexpr int kMaxMerge = 8;      // consecutive opcode-5 instructions of a layer run as one item pool
 #ifndef MK_GROUP_CHUNKS
 #define MK_GROUP_CHUNKS 7
@@ -204,7 +205,7 @@ struct KParams {
     int32_t work_sharing;
     int32_t spin_max;  // longest back-off between polls, in s_sleep(1) units
     int32_t tail_items;    // opcode-5 work sharing: items per instruction claimed through its cursor
-    int32_t early_chunks;  // opcode 6: chunks of each wave's first item loaded before the wait (<= kEarlyChunks)
+    int32_t early_loads;   // opcode 6: each wave's two first items loaded before the wait (0/1)
     int32_t pf_rounds;     // opcode 6: cache-warming rounds while opcode 5 still runs elsewhere
     // opcode 3 streams its worker's next O-projection rows into LDS while it
     // waits (stage_oproj_rows): on for the Mixtral VM, off for the dense one
@@ -805,6 +806,13 @@ __device__ __forceinline__ int next_local_item(SharedState &sh, int lane) {
     return __builtin_amdgcn_readfirstlane(v);
 }
 
+// The first of two consecutive items claimed at once.
+__device__ __forceinline__ int next_local_pair(SharedState &sh, int lane) {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&sh.next_item, 2);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
 // silu_out[e][r] = bf16(bf16(silu(bf16 g)) * bf16 u) from the wave sums of
 // the gate and up rows (lane 0 stores).
 __device__ __forceinline__ void silu_store(kp_c &p, int e, int r, float ag, float au, int lane) {
@@ -1247,8 +1255,7 @@ __device__ __forceinline__ float dot_row_regs(const RowRegs<N> &r, const u32x4 *
     return acc;
 }
 
-constexpr int kSegChunks = 16;   // max chunks per opcode-6 item (16 KiB per wave)
-constexpr int kEarlyChunks = MK_EARLY_CHUNKS;  // chunks of its first item each wave loads before the opcode-6 wait
+constexpr int kSegChunks = 16;   // chunks a dense down-projection wave loads at a time (16 KiB)
 constexpr int kRowBatch = kRowBatchLds;
 
 struct DownItem {
@@ -1263,25 +1270,43 @@ __device__ __forceinline__ DownItem down_item(int it, int S, int nc) {
     return DownItem{it / (2 * S), (it / S) & 1, c0, c1 - c0};
 }
 
-// Partial dot of one item; its first min(d.n, npre) chunks are already in
-// `pre` (npre = 0: none).
-__device__ __forceinline__ float down_item_dot(const uint16_t *row, const u32x4 *xact, const DownItem &d, int lane,
-                                               int npre, const RowRegs<kEarlyChunks> &pre) {
+// Opcode 6 streams its items through two register sets: while one item's
+// partial dot is formed, the next item's loads are in flight, so a wave
+// keeps one to two items (7-14 KiB) of loads outstanding instead of one
+// draining to none -- the bytes in flight per compute unit are what bound
+// its share of the memory bandwidth.  An item always issues kPipeChunks
+// loads (an item of fewer chunks loads its last chunk again), so the
+// compiler can count the loads still outstanding after each one and wait
+// for one register set only; 7 chunks is Mixtral's exact segment (14336
+// columns = 4 x 7 x 512).
+constexpr int kPipeChunks = 7;  // chunks per opcode-6 item (7 KiB per wave)
+constexpr int kVmcntZero = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt not waited on
+static_assert(kMaxSegments * kPipeChunks * kChunkElems >= kMaxIntermediate, "opcode-6 segments cover F");
+
+// Issues the loads of item `it` (rows [row0b, ...) of the batch) into r.
+__device__ __forceinline__ void down_item_load(kp_c &p, RowRegs<kPipeChunks> &r, int it, int S, int nc,
+                                               size_t base0, size_t base1, int row0b, int lane) {
+    const DownItem d = down_item(it, S, nc);
+    const uint16_t *row = p.down + ((d.slot ? base1 : base0) + row0b + d.row) * (size_t)p.F;
     const u32x4 *w = reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane;
-    const u32x4 *x = xact + d.c0 * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < kPipeChunks; ++i) r.w[i] = load_stream(w + min(i, d.n - 1) * 64);
+}
+
+// The partial dot of item `it` (loaded into r) with the staged SiLU row of
+// its expert slot, to sh.part[row][slot][segment].
+__device__ __forceinline__ void down_item_finish(SharedState &sh, const RowRegs<kPipeChunks> &r, const u32x4 *act,
+                                                 int nv, int it, int S, int nc, int lane) {
+    const DownItem d = down_item(it, S, nc);
+    const u32x4 *x = act + (d.slot ? nv : 0) + d.c0 * 64 + lane;
     float acc = 0.f;
-    int done = 0;
-    if (npre > 0) {
-        const int n = min(d.n, npre);
-        acc = dot_row_regs<kEarlyChunks>(pre, x, n, acc);
-        done = n;
+#pragma unroll
+    for (int i = 0; i < kPipeChunks; ++i) {  // straight-line: chunks past d.n (reloads) are dropped
+        const float t = dot8(r.w[i], x[min(i, d.n - 1) * 64], acc);
+        acc = i < d.n ? t : acc;
     }
-    if (done < d.n) {
-        RowRegs<kSegChunks> r;
-        load_row<kSegChunks>(r, w + done * 64, d.n - done);
-        acc = dot_row_regs<kSegChunks>(r, x + done * 64, d.n - done, acc);
-    }
-    return acc;
+    acc = wave_sum(acc);
+    if (lane == 0) sh.part[(d.row * 2 + d.slot) * kMaxSegments + (it % S)] = acc;
 }
 
 // Opcode 6 overlapped with the end of opcode 5 (chunk counters on, and this
@@ -1442,24 +1467,23 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = start * p.down_bs, nrows = (end - start) * p.down_bs;
     const int nc = p.F / kChunkElems;
-    const int S = (nc + kSegChunks - 1) / kSegChunks;  // column segments per row
+    const int S = (nc + kPipeChunks - 1) / kPipeChunks;  // column segments per row
 
     // Early loads: when this workgroup routed the layer itself (opcode 5 ran
     // here), the experts are known before the barrier, so each wave starts
-    // streaming the first chunks of its first item while it waits.
+    // streaming its two first items (wave and wave + 8) while it waits.
     const bool known = !(!kOverlap && p.late_loads) && sh.route_layer == layer;  // late loads: whole-model only
     if (kOverlap && p.chunk_ctr != nullptr && known && nrows <= 32 && nrows % kItemRows == 0 && (p.F % kChunkElems) == 0 &&
         nc <= kGroupChunks * kMaxGroups)
         return downproj_overlapped(p, sh, act, c, tim, layer, start, end);
     const int first_batch = min(nrows, kRowBatch);
-    const int npre_max = min(max(p.early_chunks, 0), kEarlyChunks);
-    const bool early = known && wave < first_batch * 2 * S && npre_max > 0;
-    RowRegs<kEarlyChunks> pre;
+    const bool early = known && p.early_loads != 0;
+    RowRegs<kPipeChunks> A, B;
     if (early) {
-        const DownItem d = down_item(wave, S, nc);
-        const int e = sh.route_idx[d.slot];
-        const uint16_t *row = p.down + ((size_t)(layer * p.E + e) * p.H + row0 + d.row) * (size_t)p.F;
-        load_row<kEarlyChunks>(pre, reinterpret_cast<const u32x4 *>(row) + d.c0 * 64 + lane, min(d.n, npre_max));
+        const size_t k0 = (size_t)(layer * p.E + sh.route_idx[0]) * p.H;
+        const size_t k1 = (size_t)(layer * p.E + sh.route_idx[1]) * p.H;
+        if (wave < first_batch * 2 * S) down_item_load(p, A, wave, S, nc, k0, k1, row0, lane);
+        if (wave + kWaves < first_batch * 2 * S) down_item_load(p, B, wave + kWaves, S, nc, k0, k1, row0, lane);
     }
     // The residual rows this instruction updates: when opcode 5 ran here,
     // the O-projection barrier it waited for has made them final, so they
@@ -1482,7 +1506,7 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
             __attribute__((address_space(3))) void *sink =
                 (__attribute__((address_space(3))) void *)(act + (lds_prefetch_offset(p) >> 4) + wave * 64);
             for (int m = 1; m <= p.pf_rounds; ++m) {
-                const int it = wave + m * kWaves;
+                const int it = wave + (m + 1) * kWaves;  // the items after the wave's two first
                 if (it >= first_batch * 2 * S) break;
                 const DownItem d = down_item(it, S, nc);
                 const int e = sh.route_idx[d.slot];
@@ -1522,23 +1546,52 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
         act[v] = ld_dev128(a0, (uint32_t)v * 16u);
         act[nv + v] = ld_dev128(a1, (uint32_t)v * 16u);
     }
-    if (tid == 0) sh.next_item = kWaves;
+    if (tid == 0) sh.next_item = 2 * kWaves;
     __syncthreads();
     stamp(tim, MK_TEVENT_FIRST_LOAD);
+    // Every load issued so far has landed (the early ones before the
+    // barrier polls, the activations before their LDS stores); saying so
+    // lets the compiler count the pipeline's outstanding loads exactly.
+    __builtin_amdgcn_s_waitcnt(kVmcntZero);
 
     const size_t base0 = (size_t)(layer * p.E + e0) * p.H;
     const size_t base1 = (size_t)(layer * p.E + e1) * p.H;
     for (int b0 = 0; b0 < nrows; b0 += kRowBatch) {
         const int nb_rows = min(kRowBatch, nrows - b0);
         const int items = nb_rows * 2 * S;
-        // items 0 .. kWaves-1 by wave index (their first chunks may be
-        // preloaded), the rest claimed from the LDS counter
-        for (int it = wave; it < items; it = next_local_item(sh, lane)) {
-            const DownItem d = down_item(it, S, nc);
-            const uint16_t *row = p.down + ((d.slot ? base1 : base0) + row0 + b0 + d.row) * (size_t)p.F;
-            const int npre = early && b0 == 0 && it == wave ? npre_max : 0;
-            const float acc = wave_sum(down_item_dot(row, act + (d.slot ? nv : 0), d, lane, npre, pre));
-            if (lane == 0) sh.part[(d.row * 2 + d.slot) * kMaxSegments + (it % S)] = acc;
+        // items wave and wave + kWaves first (loaded early in the first
+        // batch), then pairs of consecutive items claimed from the LDS
+        // counter (items is even, so a pair below items lies wholly in the
+        // batch; claims only grow, so the first one past it ends the
+        // loop).  At the loop head A's item, then B's, are loaded or in
+        // flight, in that order, and the loop's only exit is there: the
+        // loads are unconditional, so the compiler's count of outstanding
+        // loads is exact and each wait leaves the other set in flight (the
+        // two first items are loaded both here or both early: one set
+        // loaded early and one here would leave the count inexact).
+        const bool pre = early && b0 == 0;
+        const int rb = row0 + b0;
+        int a = __builtin_amdgcn_readfirstlane(wave), b = a + kWaves;  // uniform
+        if (b < items) {
+            if (!pre) {
+                down_item_load(p, A, a, S, nc, base0, base1, rb, lane);
+                down_item_load(p, B, b, S, nc, base0, base1, rb, lane);
+            }
+            for (;;) {
+                const int n2 = next_local_pair(sh, lane);
+                if (n2 >= items) break;
+                down_item_finish(sh, A, act, nv, a, S, nc, lane);
+                a = n2;
+                down_item_load(p, A, a, S, nc, base0, base1, rb, lane);
+                down_item_finish(sh, B, act, nv, b, S, nc, lane);
+                b = n2 + 1;
+                down_item_load(p, B, b, S, nc, base0, base1, rb, lane);
+            }
+            down_item_finish(sh, A, act, nv, a, S, nc, lane);
+            down_item_finish(sh, B, act, nv, b, S, nc, lane);
+        } else if (a < items) {
+            if (!pre) down_item_load(p, A, a, S, nc, base0, base1, rb, lane);
+            down_item_finish(sh, A, act, nv, a, S, nc, lane);
         }
         __syncthreads();
         // h = bf16(h + bf16(s_j * bf16(d_j))) for j = 0, 1 in order
@@ -1554,7 +1607,7 @@ __device__ __forceinline__ bool op_expert_downproj(kp_c &p, SharedState &sh, u32
             h = rbf(h + rbf(s1 * rbf(d1)));
             st_dev16(hp, f2bf(h));
         }
-        if (tid == 0) sh.next_item = kWaves;
+        if (tid == 0) sh.next_item = 2 * kWaves;
         __syncthreads();
     }
     drain_and_sync();
@@ -3516,7 +3569,7 @@ int validate(const mk_mixtral_globals *g) {
     if (g->num_experts_per_tok != 2 || g->num_experts < 2 || g->num_experts > MK_MAX_EXPERTS)
         return MK_ERR_UNSUPPORTED;
     if (g->hidden_size < kChunkElems || g->hidden_size % kChunkElems || g->intermediate_size < kChunkElems ||
-        g->intermediate_size % kChunkElems || g->intermediate_size > kMaxSegments * kSegChunks * kChunkElems)
+        g->intermediate_size % kChunkElems || g->intermediate_size > kMaxIntermediate)
         return MK_ERR_UNSUPPORTED;
     if (g->expert_proj_block_size < 1 || g->down_proj_block_size < 1 || g->o_proj_block_size < 1 ||
         g->intermediate_size % g->expert_proj_block_size || g->hidden_size % g->down_proj_block_size ||
@@ -3677,7 +3730,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.work_sharing = 0;
     kp.spin_max = spin_max_naps();
     kp.tail_items = tuning_value(kOvTail, MK_TAIL_ITEMS, 1, 1 << 20);
-    kp.early_chunks = tuning_value(kOvEarly, MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
+    kp.early_loads = tuning_value(kOvEarly, MK_EARLY_LOADS, 0, 1);
     kp.pf_rounds = tuning_value(kOvPf, MK_PF_ROUNDS, 0, 4);
     kp.ostage = 0;
     kp.red_cols = g->matvec_reduction_size;
@@ -3852,7 +3905,7 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.work_sharing = g->work_sharing ? 1 : 0;
     kp.spin_max = spin_max_naps();
     kp.tail_items = tuning_value(kOvTail, MK_TAIL_ITEMS, 1, 1 << 20);
-    kp.early_chunks = tuning_value(kOvEarly, MK_EARLY_CHUNKS, 0, MK_EARLY_CHUNKS);
+    kp.early_loads = tuning_value(kOvEarly, MK_EARLY_LOADS, 0, 1);
     kp.pf_rounds = tuning_value(kOvPf, MK_PF_ROUNDS, 0, 4);
     kp.ostage = 1;
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);

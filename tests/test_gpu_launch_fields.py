@@ -2,13 +2,14 @@
 
 The host fills these fields of each launch from compile-time defaults, and
 environment variables override them for measurements
-(epic-kernel_amd/csrc/mk_mixtral.hip: ``env_int``, ``spread_layout``,
+(epic-kernel_amd/csrc/mk_mixtral.hip: ``tuning_value``, ``spread_layout``,
 ``stage_limit`` and the two launch paths):
 
 * ``MK_SPIN_SLEEP``: the longest back-off between two polls of a counter;
 * ``MK_TAIL``: the opcode-5 items of an instruction that other workers of
   its group may take (work sharing);
-* ``MK_EARLY``: the opcode-6 chunks loaded into registers before the wait;
+* ``MK_EARLY``: whether opcode 6 loads each wave's two first items into
+  registers before the wait or after it;
 * ``MK_PF``: the opcode-6 cache-warming rounds;
 * ``MK_SPREAD``: which opcodes' counters are spread over per-XCD parts;
 * ``MK_STAGE_ITEMS``: the predicted or next up/gate items staged in LDS.
@@ -44,7 +45,7 @@ FIELDS = ("MK_SPIN_SLEEP", "MK_TAIL", "MK_EARLY", "MK_PF", "MK_SPREAD", "MK_STAG
 VARIANTS = [
     ("MK_SPIN_SLEEP", "1"), ("MK_SPIN_SLEEP", "64"),
     ("MK_TAIL", "1"), ("MK_TAIL", "64"), ("MK_TAIL", "4096"),
-    ("MK_EARLY", "0"), ("MK_EARLY", "4"), ("MK_EARLY", "10"),
+    ("MK_EARLY", "0"), ("MK_EARLY", "1"),
     ("MK_PF", "0"), ("MK_PF", "2"), ("MK_PF", "4"),
     ("MK_SPREAD", "0"), ("MK_SPREAD", "0x20"),
     ("MK_STAGE_ITEMS", "0"), ("MK_STAGE_ITEMS", "3"),
