@@ -2803,9 +2803,12 @@ __device__ __forceinline__ bool dense_down_rows(kp_c &p, SharedState &sh, u32x4 
 // [start, end) * down_proj_block_size (nc chunks, up to kSegChunks loads per
 // lane in flight), stored by its wave as soon as its sum is known, so only
 // the last item's store is outstanding at the end.  The first item of each
-// wave (its first kSegChunks chunks) is loaded before the wait, and, when
-// this workgroup's opcode 5 already passed the O-proj wait (the residual
-// rows are final then), so are the first kRowBatch residual rows.
+// wave (its first kSegChunks chunks) is loaded before the wait, the rows
+// after those (as many as the launch's LDS holds after the SiLU row) are
+// streamed into LDS by waves 1.. (wave 0 polls), and, when this
+// workgroup's opcode 5 already passed the O-proj wait (the residual rows
+// are final then), so are the first kRowBatch residual rows.  After the
+// wait only the SiLU row is read from memory before the sums.
 __device__ __forceinline__ bool dense_down_full(kp_c &p, SharedState &sh, u32x4 *act, const Ctx &c,
                                                 int32_t *tim, int layer, int b0, int b1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -2823,12 +2826,24 @@ __device__ __forceinline__ bool dense_down_full(kp_c &p, SharedState &sh, u32x4 
     const bool hfinal = !p.late_loads && __builtin_amdgcn_readfirstlane(sh.route_layer) == layer;
     uint32_t hpre = 0;
     if (hfinal && tid < nearly) hpre = ld_dev16(p.hidden + r0 + tid);
+    // rows kWaves .. kWaves + nst - 1, row-major 512-column chunks in lane
+    // order after the SiLU row
+    const int soff16 = ((p.F * 2 + 1023) / 1024) * 64;  // u32x4 units
+    const int nst = p.late_loads ? 0 : min(max(nrows - kWaves, 0), max(p.lds_bytes / 16 - soff16, 0) / (nc * 64));
+    if (wave >= 1)
+        for (int q = wave - 1; q < nst; q += kWaves - 1) {
+            const u32x4 *w = reinterpret_cast<const u32x4 *>(wm + (size_t)(r0 + kWaves + q) * p.F) + lane;
+            for (int ch = 0; ch < nc; ++ch)
+                __builtin_amdgcn_global_load_lds((global_void_t *)(w + ch * 64),
+                                                 (lds_void_t *)(act + soff16 + (q * nc + ch) * 64), 16, 0, 0);
+        }
     stamp(tim, MK_TEVENT_AT_GMEM_WAIT);
     if (!p.late_loads && !wait()) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     uint32_t *hrow = reinterpret_cast<uint32_t *>(sh.part);  // the residual rows read early
     if (hfinal && tid < nearly) hrow[tid] = hpre;
     for (int v = tid; v < (p.F >> 3); v += kThreads) act[v] = ld_dev128(p.silu, (uint32_t)v * 16u);
+    __builtin_amdgcn_s_waitcnt(kVmcntZero);  // this wave's staged rows have landed too
     __syncthreads();
     // the rest of row r0 + it from chunk `done` on, added to acc
     auto row_rest = [&](int it, int done, float acc) {
@@ -2855,7 +2870,14 @@ __device__ __forceinline__ bool dense_down_full(kp_c &p, SharedState &sh, u32x4 
         if (lane == 0) store_row(wave, acc);
     }
     for (int it = next_local_item(sh, lane); it < nrows; it = next_local_item(sh, lane)) {
-        const float acc = wave_sum(row_rest(it, 0, 0.f));
+        float acc = 0.f;
+        if (it - kWaves < nst) {  // the same chunk order as row_rest
+            const u32x4 *s = act + soff16 + (it - kWaves) * nc * 64 + lane;
+            for (int ch = 0; ch < nc; ++ch) acc = dot8(s[ch * 64], act[lane + ch * 64], acc);
+        } else {
+            acc = row_rest(it, 0, 0.f);
+        }
+        acc = wave_sum(acc);
         if (lane == 0) store_row(it, acc);
     }
     drain_and_sync();
