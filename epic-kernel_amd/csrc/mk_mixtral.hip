@@ -284,6 +284,7 @@ struct SharedState {
     int route_idx[2];
     float route_score[2];  // bf16 score values widened to fp32
     int flag;
+    uint32_t touch[2];  // landing words of the next-instruction touch (never read)
     int next_item;  // per-instruction item counter shared by the waves
     float part[kRowBatchLds * 2 * kMaxSegments];  // opcode-6 partial sums: [row][slot][segment]
     // opcode-5 instructions of this worker's group for the current layer, in
@@ -434,6 +435,19 @@ __device__ __forceinline__ uint32_t norm2(uint32_t x, uint32_t w, float r) {
 
 __device__ __forceinline__ void stamp(int32_t *t, int slot) {
     if (t != nullptr && threadIdx.x == 0) t[slot] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
+}
+
+// The next instruction's two 64-byte lines, read once into L2 by lanes 0
+// and 1 of the last wave (a 4-byte global_load_lds writes the word of lane
+// i at the LDS base + 4 i: sh.touch[0..1], never read): the scalar loads
+// that fetch it when its turn comes then find it there instead of in
+// memory.
+__device__ __forceinline__ void touch_next_instruction(kp_c &p, SharedState &sh, ins_t *ins, int q) {
+    const int t = (int)threadIdx.x - (kThreads - 64);
+    if (q + 1 < p.queue_len && t >= 0 && t < 2) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(ins + MK_INTS_PER_INSTRUCTION) + (uintptr_t)t * 64u;
+        __builtin_amdgcn_global_load_lds((global_void_t *)a, (lds_void_t *)sh.touch, 4, 0, 0);
+    }
 }
 
 __device__ __forceinline__ int32_t *bar_at(kp_c &p, int layer, int opcode) {
@@ -3137,6 +3151,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
         const int op = __builtin_amdgcn_readfirstlane(ins[0]);
         const Ctx c{w, q};
         stamp(tim, MK_TEVENT_START);
+        touch_next_instruction(p, sh, ins, q);
         bool ok = true;
         switch (op) {
         case 0: break;
@@ -3197,6 +3212,7 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams) {
         const int op = __builtin_amdgcn_readfirstlane(ins[0]);
         const Ctx c{w, q};
         stamp(tim, MK_TEVENT_START);
+        touch_next_instruction(p, sh, ins, q);
         bool ok = true;
         switch (op) {
         case 0: break;
