@@ -2124,6 +2124,7 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
 
     stamp(tim, MK_TEVENT_AT_GMEM_STORE);  // wave 0's positions done
     // fold the token slots of the wave (lanes with the same dp) to the wave max
+    const bool packed = G == 16;  // uniform: head dim 128, four slots = the wave's four rows of 16 lanes
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
         // partners at lane distance 8 (head dim 64 only), 16 and 32
@@ -2140,8 +2141,10 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
             const int o = 8 << k;
             if (o < G) continue;
             L[h] += lane_xor(L[h], o, lane);
+            if (!packed) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] += lane_xor(acc[h][j], o, lane);
+                for (int j = 0; j < 8; ++j) acc[h][j] += lane_xor(acc[h][j], o, lane);
+            }
         }
         M[h] = mw;
     }
@@ -2156,7 +2159,32 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
             wl[wave * GQA + h] = L[h];
         }
     }
-    if (slot == 0) {
+    if (packed) {
+        // The four rows' acc summed two registers per swap: v_permlane32_swap
+        // of (a_j, a_{j+4}) plus an add leaves a_j in the lower half and
+        // a_{j+4} in the upper (rows 0+2 and 1+3 added); v_permlane16_swap of
+        // (s_j, s_{j+2}) plus an add leaves in row r the whole sum of a_{j+2r}.
+        // Row r of t0, t1 then holds dims dp * 8 + 2r, + 1: every lane
+        // stores two.  Six swaps per head where lane exchanges take sixteen.
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+            float s[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[h][j]),
+                                                                __float_as_uint(acc[h][j + 4]), false, false);
+                s[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            }
+            float t[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[j]), __float_as_uint(s[j + 2]),
+                                                                false, false);
+                t[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            }
+            *reinterpret_cast<float2 *>(wacc + (wave * GQA + h) * D + dp * 8 + 2 * slot) = make_float2(t[0], t[1]);
+        }
+    } else if (slot == 0) {
 #pragma unroll
         for (int h = 0; h < GQA; ++h)
 #pragma unroll
