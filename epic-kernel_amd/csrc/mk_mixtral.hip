@@ -2334,31 +2334,52 @@ __device__ __forceinline__ bool op_attn_reduction(kp_c &p, SharedState &sh, u32x
     }
     __syncthreads();
     stamp(tim, 52);  // the weights are in LDS
-    for (int i = threadIdx.x; i < gqa * D; i += kThreads) {
-        const int hl = i / D, h = hs + hl, d = i % D;
+    // Four threads per (head, 4 dims): thread sub takes the partials sub,
+    // sub + 4, ... with 16-byte loads (at most 16 in flight, all issued
+    // before the first is used), then the quad adds its four sums
+    // (quad_perm DPP) and its first thread stores the 4 outputs.
+    const int ng = gqa * (D >> 2);
+    for (int t = threadIdx.x; t < 4 * ng; t += kThreads) {  // whole quads: 4 * ng is a multiple of 4
+        const int g = t >> 2, sub = t & 3;
+        const int hl = g / (D >> 2), h = hs + hl, d = (g % (D >> 2)) * 4;
         const float *f = wts + hl * 64;
-        float num = 0.f;
-        // the partials in groups of 32 loads in flight (one round trip for up
-        // to 32 partitions): every slot index first, then every load; a
-        // group's missing entries load the last slot again and add nothing
-        for (int k = 0; k < cnt; k += 32) {
-            int sl[32];
+        u32x4 v[16];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) sl[u] = range ? min(k + u, cnt - 1) : slots[min(k + u, cnt - 1)];
-            float v[32];
-#pragma unroll
-            for (int u = 0; u < 32; ++u)
-                v[u] = __uint_as_float(ld_dev32_at(a.out_int, (uint32_t)(((h * a.P + sl[u]) * D + d) * 4)));
-#pragma unroll
-            for (int u = 0; u < 32; ++u)
-                if (k + u < cnt) num = fmaf(v[u], f[k + u], num);
+        for (int u = 0; u < 16; ++u) {
+            const int kk = sub + 4 * u;
+            if (kk < cnt) {
+                const int s = range ? kk : slots[kk];
+                v[u] = ld_dev128(a.out_int, (uint32_t)(((h * a.P + s) * D + d) * 4));
+            }
         }
-        const float red = num / den[hl];
-        if (terminal) {
-            st_dev16(a.attn_out + h * D + d, f2bf(red));
-        } else {
-            st_dev32(a.out_int + ((size_t)h * a.P + out_slot) * D + d, __float_as_uint(red));
-            if (d == 0) st_dev32(a.lse_int + (size_t)h * a.P + out_slot, __float_as_uint(logf(den[hl])));
+        float num[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int kk = sub + 4 * u;
+            if (kk < cnt) {
+                const float w = f[kk];
+                num[0] = fmaf(__uint_as_float(v[u].x), w, num[0]);
+                num[1] = fmaf(__uint_as_float(v[u].y), w, num[1]);
+                num[2] = fmaf(__uint_as_float(v[u].z), w, num[2]);
+                num[3] = fmaf(__uint_as_float(v[u].w), w, num[3]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            num[j] += dpp_add_src<0xb1>(num[j]);  // quad_perm [1, 0, 3, 2]
+            num[j] += dpp_add_src<0x4e>(num[j]);  // quad_perm [2, 3, 0, 1]
+        }
+        if (sub == 0) {
+            const float dn = den[hl];
+            if (terminal) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) st_dev16(a.attn_out + h * D + d + j, f2bf(num[j] / dn));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    st_dev32(a.out_int + ((size_t)h * a.P + out_slot) * D + d + j, __float_as_uint(num[j] / dn));
+                if (d == 0) st_dev32(a.lse_int + (size_t)h * a.P + out_slot, __float_as_uint(logf(den[hl])));
+            }
         }
     }
     stamp(tim, 53);  // thread 0's sums done and stored
