@@ -3072,22 +3072,31 @@ __device__ __forceinline__ void exit_argmax(kp_c &p, SharedState &sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int V = a.V, nv = V >> 3;
     ArgBest best{0.f, -1, false};
-    // 16 B per lane, four loads in flight per thread
-    for (int base = 0; base < nv; base += 4 * kThreads) {
-        u32x4 x[4];
+    // 16 B per lane, up to 16 loads in flight per thread (one round trip
+    // for up to 64 K logits); a thread visits its indices in increasing
+    // order, so a later value replaces its best only if it is larger, or
+    // the first NaN
+    constexpr int kArgLoads = 16;
+    for (int base = 0; base < nv; base += kArgLoads * kThreads) {
+        u32x4 x[kArgLoads];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kArgLoads; ++k) {
             const int v = base + k * kThreads + tid;
-            x[k] = v < nv ? ld_dev128(a.logits, (uint32_t)v * 16u) : u32x4{0u, 0u, 0u, 0u};
+            if (v < nv) x[k] = ld_dev128(a.logits, (uint32_t)v * 16u);
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kArgLoads; ++k) {
             const int v = base + k * kThreads + tid;
             if (v < nv) {
+                const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    arg_take(best, bf2f(x[k][j] & 0xffffu), 8 * v + 2 * j);
-                    arg_take(best, bf2f(x[k][j] >> 16), 8 * v + 2 * j + 1);
+                for (int j = 0; j < 8; ++j) {
+                    const float f = bf2f((w[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                    const int i = 8 * v + j;
+                    const bool take = !best.nan && (f != f || best.idx < 0 || f > best.v);
+                    best.nan = best.nan || f != f;
+                    best.v = take ? f : best.v;
+                    best.idx = take ? i : best.idx;
                 }
             }
         }
@@ -3147,8 +3156,14 @@ __device__ __forceinline__ void kernel_exit(kp_c &p, SharedState &sh) {
     if (sh.flag) {
         if (p.argmax_out != nullptr && p.attn && !aborted(p)) exit_argmax(p, sh);
         // spread counters: their parts back into the barrier tensor (which
-        // then holds what the reference's counters would), parts zeroed
-        if (p.spread != nullptr) {
+        // then holds what the reference's counters would), parts zeroed; a
+        // launch that zeroes the barrier tensor for the next one only
+        // zeroes the parts (stores, no round trip)
+        if (p.spread != nullptr && p.reset_next > 0) {
+            for (int row = threadIdx.x; row < p.spread_rows; row += kThreads)
+#pragma unroll
+                for (int k = 0; k < kSpread; ++k) st_dev32(p.spread + (size_t)k * p.spread_stride + row, 0u);
+        } else if (p.spread != nullptr) {
             for (int row = threadIdx.x; row < p.spread_rows; row += kThreads) {
                 int sum = 0;
 #pragma unroll
@@ -3157,7 +3172,7 @@ __device__ __forceinline__ void kernel_exit(kp_c &p, SharedState &sh) {
                     sum += (int)ld_dev32(q);
                     st_dev32(q, 0u);
                 }
-                if (sum != 0 && p.reset_next == 0) {
+                if (sum != 0) {
                     int32_t *b = p.bar + (size_t)row * p.bar_width;
                     st_dev32(b, ld_dev32(b) + (uint32_t)sum);
                 }
