@@ -243,6 +243,10 @@ struct KParams {
     // that are complete instead of waiting for the whole layer
     int32_t *chunk_ctr;
     int32_t scratch_clear;  // scratch ints from kScratchSlotBase the last workgroup zeroes
+    // dense VM with argmax_out: per workgroup (value, index) of the best
+    // logit its LM-head instructions wrote (2 ints each), which the exit
+    // argmax reduces instead of reading every logit; null: read the logits
+    int32_t *lm_cand;
     // spread layer counters (NULL: off): kSpread parts of spread_rows
     // (layer, opcode) rows, spread_stride ints apart
     int32_t *spread;
@@ -285,6 +289,8 @@ struct SharedState {
     float route_score[2];  // bf16 score values widened to fp32
     int flag;
     uint32_t touch[2];  // landing words of the next-instruction touch (never read)
+    float lm_v;  // the best logit this workgroup's dense LM-head rows produced (lm_idx -1: none)
+    int lm_idx;
     int next_item;  // per-instruction item counter shared by the waves
     float part[kRowBatchLds * 2 * kMaxSegments];  // opcode-6 partial sums: [row][slot][segment]
     // opcode-5 instructions of this worker's group for the current layer, in
@@ -2972,6 +2978,49 @@ __device__ __forceinline__ bool op_dense_down(kp_c &p, SharedState &sh, u32x4 *a
     }
 }
 
+// Running argmax in torch.argmax's order: NaN above every number, then the
+// larger value, then the lower index (idx < 0: empty).
+struct ArgBest {
+    float v;
+    int idx;
+    bool nan;
+};
+
+__device__ __forceinline__ bool arg_better(const ArgBest &b, const ArgBest &a) {
+    if (b.idx < 0) return false;
+    if (a.idx < 0) return true;
+    if (a.nan || b.nan) return a.nan && b.nan ? b.idx < a.idx : b.nan;
+    return b.v > a.v || (b.v == a.v && b.idx < a.idx);
+}
+
+__device__ __forceinline__ void arg_take(ArgBest &a, float v, int idx) {
+    const ArgBest b{v, idx, v != v};
+    if (arg_better(b, a)) a = b;
+}
+
+// The waves' best logits of a dense LM-head instruction (one ArgBest per
+// wave, in lane 0) merged into the workgroup's running best (sh.lm_v,
+// sh.lm_idx), which kernel_exit publishes for the exit argmax.  Ends with a
+// workgroup barrier.
+__device__ __forceinline__ void lm_best_merge(SharedState &sh, const ArgBest &wb) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        sh.red[wave] = wb.v;
+        sh.wave_cnt[wave] = wb.idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ArgBest r{sh.lm_v, sh.lm_idx, sh.lm_v != sh.lm_v};
+        for (int w = 0; w < kWaves; ++w) {
+            const ArgBest o{sh.red[w], sh.wave_cnt[w], sh.red[w] != sh.red[w]};
+            if (arg_better(o, r)) r = o;
+        }
+        sh.lm_v = r.v;
+        sh.lm_idx = r.idx;
+    }
+    __syncthreads();
+}
+
 // Opcode 7, RMS_LM_Head [7, start, end]: RMSNorm with the LM-head norm, then
 // logits[r] = bf16(W[r] . normed) over all hidden columns for rows
 // [start, end) * lm_head_block_size, stored (not accumulated) with one
@@ -2991,10 +3040,15 @@ __device__ __forceinline__ bool dense_lm_head_rows(kp_c &p, SharedState &sh, u32
     if (!p.late_loads && !wait_ge(p, sh, bar_at(p, last, 6), p.down_arrivals, c, 7, last)) return false;
     stamp(tim, MK_TEVENT_DONE_GMEM_WAIT);
     rms_to_lds(p, sh, act, a.lm_norm);
+    ArgBest wb{0.f, -1, false};  // lane 0: the wave's best stored logit
     rows_matvec<NR, NC>(sh, w, a.lm_head, (size_t)p.H, 0, act, r0, nrows, [&](int r, float sa, float sb) {
-        st_dev32(a.logits + r, f2bf(sa) | (f2bf(sb) << 16));
+        const uint32_t ba = f2bf(sa), bb = f2bf(sb);
+        st_dev32(a.logits + r, ba | (bb << 16));
+        arg_take(wb, bf2f(ba), r);
+        arg_take(wb, bf2f(bb), r + 1);
     });
     drain_and_sync();
+    if (p.lm_cand != nullptr) lm_best_merge(sh, wb);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
 }
@@ -3028,6 +3082,7 @@ __device__ __forceinline__ bool op_dense_lm_head(kp_c &p, SharedState &sh, u32x4
     stamp(tim, MK_TEVENT_FIRST_LOAD);
     // other hidden sizes: a row pair per item
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    ArgBest wb{0.f, -1, false};  // lane 0: the wave's best stored logit
     for (int it = wave; 2 * it < nrows; it = next_local_item(sh, lane)) {
         const int ra = r0 + 2 * it;
         float aa = 0.f, ab = 0.f;
@@ -3035,31 +3090,17 @@ __device__ __forceinline__ bool op_dense_lm_head(kp_c &p, SharedState &sh, u32x4
                  aa, ab);
         aa = wave_sum(aa);
         ab = wave_sum(ab);
-        if (lane == 0) st_dev32(a.logits + ra, f2bf(aa) | (f2bf(ab) << 16));
+        if (lane == 0) {
+            const uint32_t ba = f2bf(aa), bb = f2bf(ab);
+            st_dev32(a.logits + ra, ba | (bb << 16));
+            arg_take(wb, bf2f(ba), ra);
+            arg_take(wb, bf2f(bb), ra + 1);
+        }
     }
     drain_and_sync();
+    if (p.lm_cand != nullptr) lm_best_merge(sh, wb);
     stamp(tim, MK_TEVENT_DONE_GMEM_STORE);
     return true;
-}
-
-// Running argmax in torch.argmax's order: NaN above every number, then the
-// larger value, then the lower index (idx < 0: empty).
-struct ArgBest {
-    float v;
-    int idx;
-    bool nan;
-};
-
-__device__ __forceinline__ bool arg_better(const ArgBest &b, const ArgBest &a) {
-    if (b.idx < 0) return false;
-    if (a.idx < 0) return true;
-    if (a.nan || b.nan) return a.nan && b.nan ? b.idx < a.idx : b.nan;
-    return b.v > a.v || (b.v == a.v && b.idx < a.idx);
-}
-
-__device__ __forceinline__ void arg_take(ArgBest &a, float v, int idx) {
-    const ArgBest b{v, idx, v != v};
-    if (arg_better(b, a)) a = b;
 }
 
 // Decode-driver tail of a launch, run by the last workgroup to exit (every
@@ -3072,36 +3113,46 @@ __device__ __forceinline__ void exit_argmax(kp_c &p, SharedState &sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int V = a.V, nv = V >> 3;
     ArgBest best{0.f, -1, false};
-    // 16 B per lane, up to 16 loads in flight per thread (one round trip
-    // for up to 64 K logits); a thread visits its indices in increasing
-    // order, so a later value replaces its best only if it is larger, or
-    // the first NaN
-    constexpr int kArgLoads = 16;
-    for (int base = 0; base < nv; base += kArgLoads * kThreads) {
-        u32x4 x[kArgLoads];
-#pragma unroll
-        for (int k = 0; k < kArgLoads; ++k) {
-            const int v = base + k * kThreads + tid;
-            if (v < nv) x[k] = ld_dev128(a.logits, (uint32_t)v * 16u);
+    if (p.lm_cand != nullptr) {
+        // every workgroup's best stored logit (kernel_exit published them
+        // before counting out)
+        for (int w = tid; w < (int)gridDim.x; w += kThreads) {
+            const float v = __uint_as_float(ld_dev32(p.lm_cand + 2 * w));
+            const ArgBest o{v, (int)ld_dev32(p.lm_cand + 2 * w + 1), v != v};
+            if (arg_better(o, best)) best = o;
         }
+    } else {
+        // 16 B per lane, up to 16 loads in flight per thread (one round trip
+        // for up to 64 K logits); a thread visits its indices in increasing
+        // order, so a later value replaces its best only if it is larger, or
+        // the first NaN
+        constexpr int kArgLoads = 16;
+        for (int base = 0; base < nv; base += kArgLoads * kThreads) {
+            u32x4 x[kArgLoads];
 #pragma unroll
-        for (int k = 0; k < kArgLoads; ++k) {
-            const int v = base + k * kThreads + tid;
-            if (v < nv) {
-                const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+            for (int k = 0; k < kArgLoads; ++k) {
+                const int v = base + k * kThreads + tid;
+                if (v < nv) x[k] = ld_dev128(a.logits, (uint32_t)v * 16u);
+            }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float f = bf2f((w[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                    const int i = 8 * v + j;
-                    const bool take = !best.nan && (f != f || best.idx < 0 || f > best.v);
-                    best.nan = best.nan || f != f;
-                    best.v = take ? f : best.v;
-                    best.idx = take ? i : best.idx;
+            for (int k = 0; k < kArgLoads; ++k) {
+                const int v = base + k * kThreads + tid;
+                if (v < nv) {
+                    const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float f = bf2f((w[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                        const int i = 8 * v + j;
+                        const bool take = !best.nan && (f != f || best.idx < 0 || f > best.v);
+                        best.nan = best.nan || f != f;
+                        best.v = take ? f : best.v;
+                        best.idx = take ? i : best.idx;
+                    }
                 }
             }
         }
+        for (int i = 8 * nv + tid; i < V; i += kThreads) arg_take(best, bf2f(ld_dev16(a.logits + i)), i);
     }
-    for (int i = 8 * nv + tid; i < V; i += kThreads) arg_take(best, bf2f(ld_dev16(a.logits + i)), i);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
         const ArgBest o{__shfl_xor(best.v, m), __shfl_xor(best.idx, m), __shfl_xor((int)best.nan, m) != 0};
@@ -3147,6 +3198,10 @@ __device__ __forceinline__ void zero_words(uint32_t *p, size_t n) {
 // when one was asked for.  Every other workgroup has finished all of its
 // scratch accesses before it increments the counter.
 __device__ __forceinline__ void kernel_exit(kp_c &p, SharedState &sh) {
+    if (p.lm_cand != nullptr && threadIdx.x == 0) {
+        st_dev32(p.lm_cand + 2 * blockIdx.x, __float_as_uint(sh.lm_v));
+        st_dev32(p.lm_cand + 2 * blockIdx.x + 1, (uint32_t)sh.lm_idx);
+    }
     drain_and_sync();
     if (threadIdx.x == 0) {
         const int prev = __hip_atomic_fetch_add(p.scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3204,6 +3259,8 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
         sh.route_layer = -1;
         sh.stage_slot = -1;
         sh.ostage_slot = -1;
+        sh.lm_v = 0.f;
+        sh.lm_idx = -1;
     }
     __syncthreads();
 
@@ -3265,6 +3322,8 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams) {
         sh.route_layer = -1;
         sh.stage_slot = -1;
         sh.ostage_slot = -1;
+        sh.lm_v = 0.f;
+        sh.lm_idx = -1;
     }
     __syncthreads();
 
@@ -3792,18 +3851,24 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     const size_t stage_items = stage_limit(
         lds_cap > stage_off ? std::min((size_t)MK_STAGE_ITEMS, (lds_cap - stage_off) / stage_item) : 0, g->late_loads);
     if (stage_items > 0) lds = std::max(lds, stage_off + stage_items * stage_item);
-    const SpreadLayout sp = spread_layout(kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len,
-                                          g->num_layers, g->bar_ops, kSpreadDenseOps);
+    // scratch: the work-claim slots, then the exit argmax's candidates (2
+    // ints per workgroup), then the spread counters
+    const size_t cand = kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len;
+    const SpreadLayout sp = spread_layout(cand + 2 * (size_t)g->num_workers, g->num_layers, g->bar_ops,
+                                          kSpreadDenseOps);
     rc = ensure_scratch(st, sp.end);
     if (rc != MK_OK) return rc;
 
     KParams kp{};
     kp.chunk_ctr = nullptr;
+    kp.lm_cand = g->argmax_out != nullptr ? st->scratch + cand : nullptr;
     kp.spread = sp.on ? st->scratch + sp.offset : nullptr;
     kp.spread_rows = (int32_t)sp.rows;
     kp.spread_stride = (int32_t)sp.stride;
     kp.spread_ops = sp.ops;
-    kp.scratch_clear = (int32_t)(2 * (size_t)g->num_workers * (size_t)g->queue_len);
+    // the last workgroup zeroes the claim slots and the candidates (after
+    // the exit argmax has read them): every launch starts from zeroed scratch
+    kp.scratch_clear = (int32_t)(cand + 2 * (size_t)g->num_workers - kScratchSlotBase);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
     kp.bar = g->barriers;
@@ -3966,7 +4031,7 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
         base = st->scratch;
     }
 
-    KParams kp;
+    KParams kp{};  // every field the launch does not set is zero (null lm_cand: the exit argmax reads the logits)
     kp.chunk_ctr = overlap ? base + kScratchSlotBase + cursors : nullptr;
     kp.spread = sp.on ? base + sp.offset : nullptr;
     kp.spread_rows = (int32_t)sp.rows;
