@@ -1989,6 +1989,7 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
     const int t0 = tb0 * a.kv_bs, t1 = min(tb1 * a.kv_bs, seq);
     const int nch = t1 > t0 ? (t1 - t0 + CT - 1) / CT : 0;
     const int first = t0 + wave * TPW + slot;  // this lane's position in chunk 0
+    const int wpos = t0 + __builtin_amdgcn_readfirstlane(wave) * TPW;  // the wave's first position in chunk 0
     const bool has_new = pos >= t0 && pos < t1;
     const int c_new = has_new ? (pos - t0) / CT : -1;
     const bool own_new = has_new && ((pos - t0) % CT) / TPW == wave;  // uniform
@@ -2075,7 +2076,10 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
 #pragma unroll
         for (int u = 0; u < kAttnSub; ++u) {
             const int ch = cg + u, k = ch % nb;
-            const bool live = ch < nch;  // uniform
+            // chunks where every position of this wave is past the
+            // partition (the last one, partly filled) are skipped: their
+            // scores are -inf and their terms zero (uniform per wave)
+            const bool live = ch < nch && wpos + ch * CT < t1;
             const bool valid = live && first + ch * CT < t1;
             float kf[8];
             if (live) widen8(kl[k * (kKvChunkBytes / 16)], kf);
@@ -2107,7 +2111,7 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
 #pragma unroll
         for (int u = 0; u < kAttnSub; ++u) {
             const int ch = cg + u, k = ch % nb;
-            if (ch >= nch) continue;  // uniform
+            if (ch >= nch || wpos + ch * CT >= t1) continue;  // uniform per wave, as above
             // rows staged for masked positions may hold anything
             // (the row pos_id is read before this launch writes it)
             const u32x4 vraw = first + ch * CT < t1 ? kl[k * (kKvChunkBytes / 16) + kKvChunkBytes / 32]
