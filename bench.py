@@ -57,11 +57,11 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes moved per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE per
 # dispatch, each scaled by what the same counter reads for a device copy of
 # known size: FETCH x 2.0, WRITE x 1.0), measured on the kernel of commit
-# 32d375a: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
+# d166c1c: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
 # 4098 / 16386 cached positions.  The counter runs are summarised under
 # profiles/.
-MEASURED_TRAFFIC_BYTES = {"c2": 708_295_877, "c3": 6_730_852_216, "c4": 26_326_975_555, "c5": 27_932_303_669}
-TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 32d375a; "
+MEASURED_TRAFFIC_BYTES = {"c2": 707_544_839, "c3": 6_733_777_962, "c4": 26_295_866_544, "c5": 27_966_525_367}
+TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit d166c1c; "
                 "configs 3-5 at 2050 / 4098 / 16386 cached positions)")
 
 
