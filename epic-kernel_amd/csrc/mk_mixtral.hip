@@ -3248,7 +3248,7 @@ __device__ __forceinline__ void kernel_exit(kp_c &p, SharedState &sh) {
             }
         }
         // work-sharing cursors, then the column-chunk counters
-        for (int i = threadIdx.x; i < p.scratch_clear; i += kThreads) p.scratch[kScratchSlotBase + i] = 0;
+        zero_words(reinterpret_cast<uint32_t *>(p.scratch + kScratchSlotBase), (size_t)p.scratch_clear);
         drain_and_sync();
         if (threadIdx.x == 0) __hip_atomic_store(p.scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
