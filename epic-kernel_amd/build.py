@@ -16,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -32,7 +33,59 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -> Path:
+# Kernel symbol (as the compiler names it) -> the macro that carries its
+# machine-code length into the host code (code_prefetch's bound).
+KERNELS = {
+    "_ZN12_GLOBAL__N_115mk_llama_kernelENS_7KParamsE": "MK_CODE_LEN_LLAMA",
+    "_ZN12_GLOBAL__N_117mk_mixtral_kernelILi8ELb1EEEvNS_7KParamsE": "MK_CODE_LEN_E8_ATTN",
+    "_ZN12_GLOBAL__N_117mk_mixtral_kernelILi0ELb1EEEvNS_7KParamsE": "MK_CODE_LEN_E0_ATTN",
+    "_ZN12_GLOBAL__N_117mk_mixtral_kernelILi8ELb0EEEvNS_7KParamsE": "MK_CODE_LEN_E8",
+    "_ZN12_GLOBAL__N_117mk_mixtral_kernelILi0ELb0EEEvNS_7KParamsE": "MK_CODE_LEN_E0",
+}
+# kernel_code_base() rounds the program counter down to the kernel's
+# 256-byte-aligned entry, so its s_getpc_b64 must sit in the first 256 bytes:
+# at most this many instructions (12 bytes at most each) before it.
+MAX_INSNS_BEFORE_GETPC = 20
+
+
+def code_lengths(asm: str) -> dict[str, int]:
+    """Machine-code length of every kernel in the device assembly, and a
+    check that each kernel reads its program counter within its first 256
+    bytes."""
+    lengths: dict[str, int] = {}
+    current = None
+    before = None  # instructions seen before s_getpc_b64 in the current kernel
+    for line in asm.splitlines():
+        if "codeLenInByte" in line:
+            if current is not None:
+                if before is not None:
+                    raise RuntimeError(f"{current}: no s_getpc_b64 near the entry")
+                lengths[current] = int(line.split("=")[1])
+            current = None
+            continue
+        head = line.split(";", 1)[0].strip()
+        if not head or head.startswith("."):
+            continue
+        if head.endswith(":"):
+            if head[:-1] in KERNELS:
+                current, before = head[:-1], 0
+            continue
+        if current is not None and before is not None:
+            if head.startswith("s_getpc_b64"):
+                if before > MAX_INSNS_BEFORE_GETPC:
+                    raise RuntimeError(f"{current}: {before} instructions before s_getpc_b64")
+                before = None
+            else:
+                before += 1
+    missing = set(KERNELS) - set(lengths)
+    if missing:
+        raise RuntimeError(f"no code length for {sorted(missing)}")
+    return lengths
+
+
+def compile_once(out: Path, defines: dict, verbose: bool) -> dict[str, int]:
+    """One hipcc compile of the library into `out`; returns the kernels'
+    machine-code lengths from the device assembly of that same compile."""
     cmd = [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -40,6 +93,7 @@ def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -
         "-std=c++17",
         "-fPIC",
         "-shared",
+        "-save-temps",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         # every atomic in the kernel is issued by one lane; the wave-aggregating
         # rewrite would broadcast each result right after the atomic and so
@@ -47,16 +101,34 @@ def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -
         "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
         f"-I{REPO / 'include'}",
     ]
-    for k, v in (defines or {}).items():
+    for k, v in defines.items():
         cmd.append(f"-D{k}={v}")
-    tmp = out.with_name(out.name + ".tmp")
-    cmd += ["-o", str(tmp), str(SRC)]
+    cmd += ["-o", str(out), str(SRC)]
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {out.name}")
+    with tempfile.TemporaryDirectory(prefix="mk_build_") as tmp:
+        res = subprocess.run(cmd, capture_output=True, text=True, cwd=tmp)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"hipcc failed ({res.returncode}) building {out.name}")
+        asm = Path(tmp) / f"{SRC.stem}-hip-amdgcn-amd-amdhsa-{ARCH}.s"
+        return code_lengths(asm.read_text())
+
+
+def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -> Path:
+    """Compile the library twice: the first compile measures each kernel's
+    machine-code length, the second passes the lengths to the host code.
+    The device code does not depend on them, so both compiles must give the
+    same lengths (checked)."""
+    defines = dict(defines or {})
+    tmp = out.with_name(out.name + ".tmp")
+    first = compile_once(tmp, defines, verbose)
+    lens = {KERNELS[k]: n for k, n in first.items()}
+    if verbose:
+        print("machine-code bytes:", lens, flush=True)
+    second = compile_once(tmp, {**defines, **lens}, verbose)
+    if second != first:
+        raise RuntimeError(f"device code changed between the two compiles: {first} vs {second}")
     os.replace(tmp, out)
     return out
 

@@ -97,6 +97,26 @@
 #ifndef MK_STAGE_ITEMS
 #define MK_STAGE_ITEMS 16
 #endif
+// Machine-code bytes of each kernel, read into L2 as the kernel runs
+// (code_prefetch).  The build measures them from the compiler's output of
+// the same source and compiles the library a second time with them; only
+// host code uses them, so the device code of both compiles is identical.
+// 0: no prefetch (a library compiled in one pass).
+#ifndef MK_CODE_LEN_LLAMA
+#define MK_CODE_LEN_LLAMA 0
+#endif
+#ifndef MK_CODE_LEN_E8_ATTN
+#define MK_CODE_LEN_E8_ATTN 0
+#endif
+#ifndef MK_CODE_LEN_E0_ATTN
+#define MK_CODE_LEN_E0_ATTN 0
+#endif
+#ifndef MK_CODE_LEN_E8
+#define MK_CODE_LEN_E8 0
+#endif
+#ifndef MK_CODE_LEN_E0
+#define MK_CODE_LEN_E0 0
+#endif
 
 namespace {
 
@@ -256,6 +276,9 @@ struct KParams {
     // bar_ints (< 2^16 whenever spread is set): q = umulhi(n, ceil(2^32 / d))
     uint32_t bar_width_magic, bar_ops_magic;
     int32_t bar_ints;
+    // bytes of the launched kernel's machine code that code_prefetch reads
+    // into L2 (at most the kernel's length; 0: off)
+    uint32_t code_len;
     AttnParams attn_params;  // read only through attn_of()
 };
 
@@ -288,7 +311,7 @@ struct SharedState {
     int route_idx[2];
     float route_score[2];  // bf16 score values widened to fp32
     int flag;
-    uint32_t touch[2];  // landing words of the next-instruction touch (never read)
+    uint32_t touch[64];  // landing words of the next-instruction touch and the code prefetch (never read)
     float lm_v;  // the best logit this workgroup's dense LM-head rows produced (lm_idx -1: none)
     int lm_idx;
     int next_item;  // per-instruction item counter shared by the waves
@@ -454,6 +477,37 @@ __device__ __forceinline__ void touch_next_instruction(kp_c &p, SharedState &sh,
         const uintptr_t a = reinterpret_cast<uintptr_t>(ins + MK_INTS_PER_INSTRUCTION) + (uintptr_t)t * 64u;
         __builtin_amdgcn_global_load_lds((global_void_t *)a, (lds_void_t *)sh.touch, 4, 0, 0);
     }
+}
+
+// First byte of the running kernel's machine code.  Kernels start on
+// 256-byte boundaries and every kernel calls this first thing, within its
+// first 256 bytes (the build checks that in the compiler's output), so the
+// program counter rounded down to 256 bytes is the entry.
+__device__ __forceinline__ uint64_t kernel_code_base() {
+    uint64_t pc;
+    asm volatile("s_getpc_b64 %0" : "=s"(pc));
+    return pc & ~(uint64_t)255;
+}
+
+// The kernel's machine code, kept in L2: at the start of every instruction
+// the last-but-one wave reads 4 bytes of each 128-byte line of one 32nd of
+// the code (global_load_lds into sh.touch, never read), workgroup w slice
+// (w / 8 + q) mod 32, so the 32 workgroups of an XCD (blockIdx mod 8) cover
+// all of it at every round of instruction starts.  The weight stream evicts
+// the code from L2 within a layer; without this, a stage's first
+// instructions wait ~0.9 us for each instruction-cache line from HBM (about
+// 185,000 instruction-cache misses per config-4 step), on the critical path
+// of whichever workgroup finished the previous stage last.  Reads stay
+// below code + p.code_len, at most the kernel's length.
+__device__ __forceinline__ void code_prefetch(kp_c &p, SharedState &sh, uint64_t code, int q) {
+    const int t = (int)threadIdx.x - (kThreads - 128);
+    const uint32_t lines = p.code_len >> 7;
+    if (lines == 0 || t < 0 || t >= 64) return;
+    const uint32_t per = (lines + 31) >> 5, j = ((uint32_t)(blockIdx.x >> 3) + (uint32_t)q) & 31u;
+    const uint32_t end = min(j * per + per, lines);
+    for (uint32_t l = j * per + (uint32_t)t; l < end; l += 64u)
+        __builtin_amdgcn_global_load_lds((global_void_t *)(code + ((uint64_t)l << 7)), (lds_void_t *)sh.touch, 4, 0,
+                                         0);
 }
 
 __device__ __forceinline__ int32_t *bar_at(kp_c &p, int layer, int opcode) {
@@ -3256,6 +3310,7 @@ __device__ __forceinline__ void kernel_exit(kp_c &p, SharedState &sh) {
 
 template <int kE, bool kAttn>
 __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
+    const uint64_t code = kernel_code_base();
     kp_c &p = kparams();
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
@@ -3277,6 +3332,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
         const Ctx c{w, q};
         stamp(tim, MK_TEVENT_START);
         touch_next_instruction(p, sh, ins, q);
+        code_prefetch(p, sh, code, q);
         bool ok = true;
         switch (op) {
         case 0: break;
@@ -3319,6 +3375,7 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
 // side is shared with the Mixtral kernel; opcodes 5-7 are the dense MLP and
 // the LM head.
 __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams) {
+    const uint64_t code = kernel_code_base();
     kp_c &p = kparams();
     extern __shared__ u32x4 act[];
     __shared__ SharedState sh;
@@ -3340,6 +3397,7 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams) {
         const Ctx c{w, q};
         stamp(tim, MK_TEVENT_START);
         touch_next_instruction(p, sh, ins, q);
+        code_prefetch(p, sh, code, q);
         bool ok = true;
         switch (op) {
         case 0: break;
@@ -3561,13 +3619,13 @@ struct SpreadLayout {
 };
 
 // Launch-time tuning overrides, for measurements: MK_SPREAD, MK_SPIN_SLEEP,
-// MK_TAIL, MK_EARLY, MK_PF and MK_STAGE_ITEMS.  The environment is read once
+// MK_TAIL, MK_EARLY, MK_PF, MK_STAGE_ITEMS and MK_CODE_PF.  The environment is read once
 // per process, at the first launch (mk_mixtral_reload_overrides reads it
 // again).  A value that is not a whole number is ignored with a warning on
 // stderr, and each override in effect is reported there when it is read, so
 // a stray variable in a serving process shows instead of silently changing
 // the scheduling.
-enum { kOvSpread, kOvSpinSleep, kOvTail, kOvEarly, kOvPf, kOvStageItems, kOvCount };
+enum { kOvSpread, kOvSpinSleep, kOvTail, kOvEarly, kOvPf, kOvStageItems, kOvCodePf, kOvCount };
 struct TuningOverride {
     const char *name;
     bool set;
@@ -3575,7 +3633,8 @@ struct TuningOverride {
 };
 TuningOverride g_overrides[kOvCount] = {{"MK_SPREAD", false, 0}, {"MK_SPIN_SLEEP", false, 0},
                                         {"MK_TAIL", false, 0},   {"MK_EARLY", false, 0},
-                                        {"MK_PF", false, 0},     {"MK_STAGE_ITEMS", false, 0}};
+                                        {"MK_PF", false, 0},     {"MK_STAGE_ITEMS", false, 0},
+                                        {"MK_CODE_PF", false, 0}};
 std::mutex g_overrides_mutex;
 bool g_overrides_read = false;
 
@@ -3640,6 +3699,15 @@ size_t stage_limit(size_t n, bool late_loads) {
     long v = 0;
     if (tuning_override(kOvStageItems, &v)) n = std::min(n, (size_t)std::max(0L, v));
     return late_loads ? 0 : n;
+}
+
+// Machine-code bytes code_prefetch reads for a kernel whose measured length
+// is `len` (0 in a library compiled without the measurement); MK_CODE_PF=0
+// turns the prefetch off for measurements.
+uint32_t code_prefetch_len(uint32_t len) {
+    long v = 1;
+    (void)tuning_override(kOvCodePf, &v);
+    return v != 0 ? len : 0u;
 }
 
 uint32_t timeout_ticks(uint32_t spin_timeout_us) {
@@ -3904,6 +3972,7 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.early_loads = tuning_value(kOvEarly, MK_EARLY_LOADS, 0, 1);
     kp.pf_rounds = tuning_value(kOvPf, MK_PF_ROUNDS, 0, 4);
     kp.ostage = 0;
+    kp.code_len = code_prefetch_len(MK_CODE_LEN_LLAMA);
     kp.red_cols = g->matvec_reduction_size;
     kp.late_loads = g->late_loads ? 1 : 0;
     kp.stage_items = (int32_t)stage_items;
@@ -4079,6 +4148,8 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.early_loads = tuning_value(kOvEarly, MK_EARLY_LOADS, 0, 1);
     kp.pf_rounds = tuning_value(kOvPf, MK_PF_ROUNDS, 0, 4);
     kp.ostage = 1;
+    kp.code_len = code_prefetch_len(e8 ? (attn ? MK_CODE_LEN_E8_ATTN : MK_CODE_LEN_E8)
+                                         : (attn ? MK_CODE_LEN_E0_ATTN : MK_CODE_LEN_E0));
     kp.down_arrivals = 2 * (g->hidden_size / g->down_proj_block_size);
     kp.red_cols = 0;
     // whole-model launches: the O projection stages up to one predicted

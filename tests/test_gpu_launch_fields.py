@@ -12,7 +12,9 @@ environment variables override them for measurements
   registers before the wait or after it;
 * ``MK_PF``: the opcode-6 cache-warming rounds;
 * ``MK_SPREAD``: which opcodes' counters are spread over per-XCD parts;
-* ``MK_STAGE_ITEMS``: the predicted or next up/gate items staged in LDS.
+* ``MK_STAGE_ITEMS``: the predicted or next up/gate items staged in LDS;
+* ``MK_CODE_PF``: whether every instruction start reads a slice of the
+  kernel's machine code into L2 (0: off).
 
 They decide when loads are issued, how long a poll sleeps, which workgroup
 computes an item and where a counter's arrivals land, never the order of
@@ -49,6 +51,7 @@ VARIANTS = [
     ("MK_PF", "0"), ("MK_PF", "2"), ("MK_PF", "4"),
     ("MK_SPREAD", "0"), ("MK_SPREAD", "0x20"),
     ("MK_STAGE_ITEMS", "0"), ("MK_STAGE_ITEMS", "3"),
+    ("MK_CODE_PF", "0"),
     ("MK_TAIL", "8x"),
 ]
 
