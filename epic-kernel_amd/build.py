@@ -121,6 +121,7 @@ def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -
     The device code does not depend on them, so both compiles must give the
     same lengths (checked)."""
     defines = dict(defines or {})
+    out = Path(out).resolve()  # the compiles run in a temporary directory
     tmp = out.with_name(out.name + ".tmp")
     first = compile_once(tmp, defines, verbose)
     lens = {KERNELS[k]: n for k, n in first.items()}
