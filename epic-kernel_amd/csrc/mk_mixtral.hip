@@ -502,6 +502,26 @@ __device__ __forceinline__ uint64_t kernel_code_base() {
 // 185,000 instruction-cache misses per config-4 step), on the critical path
 // of whichever workgroup finished the previous stage last.  Reads stay
 // below code + p.code_len, at most the kernel's length.
+// The 32 KiB of machine code that follow the program counter where this is
+// called (the handler about to run), read into L2 in one batch by the
+// third-last wave: the instruction cache's misses as the handler starts then
+// find their lines in L2 instead of fetching them from HBM one after
+// another.  Same-process A/B against code_prefetch alone: config 4 +0.3 to
+// +0.4 %, config 3 +0.2 %; 64 KiB measured 1 % slower at config 3.  Reads
+// stay inside [code, code + p.code_len).
+__device__ __forceinline__ void handler_prefetch(kp_c &p, SharedState &sh, uint64_t code) {
+    const int t = (int)threadIdx.x - (kThreads - 192);
+    if (p.code_len == 0 || t < 0 || t >= 64) return;
+    uint64_t pc;
+    asm volatile("s_getpc_b64 %0" : "=s"(pc));
+    const uint64_t end = code + (p.code_len & ~127u), base = pc & ~(uint64_t)127;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint64_t a = base + ((uint64_t)(t + 64 * k) << 7);
+        if (a < end) __builtin_amdgcn_global_load_lds((global_void_t *)a, (lds_void_t *)sh.touch, 4, 0, 0);
+    }
+}
+
 __device__ __forceinline__ void code_prefetch(kp_c &p, SharedState &sh, uint64_t code, int q) {
     const int t = (int)threadIdx.x - (kThreads - 128);
     const uint32_t lines = p.code_len >> 7;
@@ -3361,23 +3381,43 @@ __global__ void __launch_bounds__(kThreads) mk_mixtral_kernel(KParams) {
         case 0: break;
         case 5: {
             int consumed = 1;
+            handler_prefetch(p, sh, code);
             ok = op_rms_router_upgate<kE, kAttn>(p, sh, act, ins, c, tim, consumed);
             q += consumed - 1;
             break;
         }
-        case 6: ok = op_expert_downproj<kE == 8 && !kAttn>(p, sh, act, ins, c, tim); break;
-        case 8: ok = op_predict<kE>(p, sh, act, ins, c, tim); break;
+        case 6:
+            handler_prefetch(p, sh, code);
+            ok = op_expert_downproj<kE == 8 && !kAttn>(p, sh, act, ins, c, tim);
+            break;
+        case 8:
+            handler_prefetch(p, sh, code);
+            ok = op_predict<kE>(p, sh, act, ins, c, tim);
+            break;
         case 1:
         case 2:
         case 3:
         case 4:
         case 7:
             if constexpr (kAttn) {
-                if (op == 1) ok = op_qkv(p, sh, act, ins, c, tim);
-                else if (op == 2) ok = op_partial_attn(p, sh, act, ins, c, tim);
-                else if (op == 3) ok = op_attn_reduction(p, sh, act, ins, c, tim);
-                else if (op == 4) ok = op_oproj(p, sh, act, ins, c, tim);
-                else ok = op_lm_head(p, sh, act, ins, c, tim);
+                // the prefetch in each branch: its program counter is where
+                // that handler's code starts
+                if (op == 1) {
+                    handler_prefetch(p, sh, code);
+                    ok = op_qkv(p, sh, act, ins, c, tim);
+                } else if (op == 2) {
+                    handler_prefetch(p, sh, code);
+                    ok = op_partial_attn(p, sh, act, ins, c, tim);
+                } else if (op == 3) {
+                    handler_prefetch(p, sh, code);
+                    ok = op_attn_reduction(p, sh, act, ins, c, tim);
+                } else if (op == 4) {
+                    handler_prefetch(p, sh, code);
+                    ok = op_oproj(p, sh, act, ins, c, tim);
+                } else {
+                    handler_prefetch(p, sh, code);
+                    ok = op_lm_head(p, sh, act, ins, c, tim);
+                }
             } else {
                 ok = need_attention(p, c, op, __builtin_amdgcn_readfirstlane(ins[1]));
             }
@@ -3424,13 +3464,13 @@ __global__ void __launch_bounds__(kThreads) mk_llama_kernel(KParams) {
         bool ok = true;
         switch (op) {
         case 0: break;
-        case 1: ok = op_qkv(p, sh, act, ins, c, tim); break;
-        case 2: ok = op_partial_attn(p, sh, act, ins, c, tim); break;
-        case 3: ok = op_attn_reduction(p, sh, act, ins, c, tim); break;
-        case 4: ok = op_oproj(p, sh, act, ins, c, tim); break;
-        case 5: ok = op_dense_upgate(p, sh, act, ins, c, tim); break;
-        case 6: ok = op_dense_down(p, sh, act, ins, c, tim); break;
-        case 7: ok = op_dense_lm_head(p, sh, act, ins, c, tim); break;
+        case 1: handler_prefetch(p, sh, code); ok = op_qkv(p, sh, act, ins, c, tim); break;
+        case 2: handler_prefetch(p, sh, code); ok = op_partial_attn(p, sh, act, ins, c, tim); break;
+        case 3: handler_prefetch(p, sh, code); ok = op_attn_reduction(p, sh, act, ins, c, tim); break;
+        case 4: handler_prefetch(p, sh, code); ok = op_oproj(p, sh, act, ins, c, tim); break;
+        case 5: handler_prefetch(p, sh, code); ok = op_dense_upgate(p, sh, act, ins, c, tim); break;
+        case 6: handler_prefetch(p, sh, code); ok = op_dense_down(p, sh, act, ins, c, tim); break;
+        case 7: handler_prefetch(p, sh, code); ok = op_dense_lm_head(p, sh, act, ins, c, tim); break;
         default:
             report_error(p, MK_ERR_BAD_OPCODE, c, op, 0, 0, op);
             ok = false;
