@@ -186,3 +186,32 @@ def test_python_launcher_rejects_bad_arguments():
     args = [torch.empty(0)] * 17 + [torch.empty(4, dtype=torch.bfloat16)] + [torch.empty(0)] * 10
     with pytest.raises(ValueError, match="GPU"):
         mk_mixtral.build_globals_struct(*args, 0, 1.0, 1e-5, False)
+
+
+def _asm(kernel, before_getpc, length, getpc=True):
+    body = "\n".join(["\ts_mov_b32 s0, 0"] * before_getpc + (["\ts_getpc_b64 s[4:5]"] if getpc else []) +
+                     ["\ts_endpgm"])
+    return (f"\t.p2align\t8\n\t.type\t{kernel},@function\n{kernel}: ; @{kernel}\n; %bb.0:\n"
+            f"\t; a comment\n{body}\n.Lfunc_end0:\n\t.size\t{kernel}, .Lfunc_end0-{kernel}\n"
+            f"; codeLenInByte = {length}\n; NumVgprs: 10\n")
+
+
+def test_build_reads_code_lengths_and_checks_the_entry_pc():
+    """build.py's second compile hands each kernel's machine-code length to
+    the host code, for the kernel's reads of its own code: the lengths come
+    from the compiler's device assembly, and the build refuses a kernel that
+    reads its program counter too far from its entry (the rounding down to
+    the 256-byte-aligned entry would then be wrong) or not at all."""
+    import build
+
+    names = list(build.KERNELS)
+    asm = "".join(_asm(k, 3, 1000 + i) for i, k in enumerate(names))
+    assert build.code_lengths(asm) == {k: 1000 + i for i, k in enumerate(names)}
+    far = "".join(_asm(k, build.MAX_INSNS_BEFORE_GETPC + 1 if i == 2 else 0, 64) for i, k in enumerate(names))
+    with pytest.raises(RuntimeError, match="before s_getpc_b64"):
+        build.code_lengths(far)
+    missing = "".join(_asm(k, 0, 64, getpc=i != 1) for i, k in enumerate(names))
+    with pytest.raises(RuntimeError, match="no s_getpc_b64"):
+        build.code_lengths(missing)
+    with pytest.raises(RuntimeError, match="no code length"):
+        build.code_lengths("".join(_asm(k, 0, 64) for k in names[:-1]))
