@@ -57,11 +57,11 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes moved per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE per
 # dispatch, each scaled by what the same counter reads for a device copy of
 # known size: FETCH x 2.0, WRITE x 1.0), measured on the kernel of commit
-# 9fe95e1: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
+# 453451c: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
 # 4098 / 16386 cached positions.  The counter runs are summarised under
 # profiles/.
-MEASURED_TRAFFIC_BYTES = {"c2": 707_863_311, "c3": 6_772_798_358, "c4": 26_290_325_850, "c5": 28_039_613_744}
-TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 9fe95e1; "
+MEASURED_TRAFFIC_BYTES = {"c2": 707_849_888, "c3": 6_768_266_129, "c4": 26_290_276_762, "c5": 28_034_514_725}
+TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 453451c; "
                 "configs 3-5 at 2050 / 4098 / 16386 cached positions)")
 
 
