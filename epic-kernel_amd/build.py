@@ -111,8 +111,12 @@ def compile_once(out: Path, defines: dict, verbose: bool) -> dict[str, int]:
         if res.returncode != 0:
             sys.stderr.write(res.stdout + res.stderr)
             raise RuntimeError(f"hipcc failed ({res.returncode}) building {out.name}")
-        asm = Path(tmp) / f"{SRC.stem}-hip-amdgcn-amd-amdhsa-{ARCH}.s"
-        return code_lengths(asm.read_text())
+        # the device assembly hipcc keeps with -save-temps
+        # (<stem>-hip-amdgcn-amd-amdhsa-<arch>.s with ROCm 7)
+        asms = sorted(Path(tmp).glob(f"*amdgcn*{ARCH}*.s"))
+        if len(asms) != 1:
+            raise RuntimeError(f"expected one device assembly file from -save-temps, found {[a.name for a in asms]}")
+        return code_lengths(asms[0].read_text())
 
 
 def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -> Path:
