@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import os
 import shutil
+import struct
 import subprocess
 import sys
 import tempfile
@@ -83,9 +84,36 @@ def code_lengths(asm: str) -> dict[str, int]:
     return lengths
 
 
+def elf_functions(data: bytes) -> dict[str, tuple[int, int]]:
+    """(address, size) of every function symbol of a 64-bit little-endian
+    ELF file (the linked device code object)."""
+    if data[:4] != b"\x7fELF" or data[4] != 2 or data[5] != 1:
+        raise RuntimeError("not a 64-bit little-endian ELF file")
+    shoff, = struct.unpack_from("<Q", data, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    sections = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    out: dict[str, tuple[int, int]] = {}
+    for sec in sections:
+        if sec[1] != 2:  # SHT_SYMTAB
+            continue
+        strtab = sections[sec[6]]
+        for off in range(sec[4], sec[4] + sec[5], 24):
+            name_off, info, _other, _shndx, value, size = struct.unpack_from("<IBBHQQ", data, off)
+            if info & 0xF != 2:  # STT_FUNC
+                continue
+            start = strtab[4] + name_off
+            name = data[start:data.index(b"\0", start)].decode()
+            out[name] = (value, size)
+    return out
+
+
 def compile_once(out: Path, defines: dict, verbose: bool) -> dict[str, int]:
     """One hipcc compile of the library into `out`; returns the kernels'
-    machine-code lengths from the device assembly of that same compile."""
+    machine-code lengths: the sizes of their symbols in the linked device
+    code object of that same compile (the assembly's codeLenInByte is the
+    compiler's estimate before branch relaxation and can exceed them by a
+    few hundred bytes), after checking that each kernel starts on a 256-byte
+    boundary and reads its program counter within its first 256 bytes."""
     cmd = [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -114,9 +142,21 @@ def compile_once(out: Path, defines: dict, verbose: bool) -> dict[str, int]:
         # the device assembly hipcc keeps with -save-temps
         # (<stem>-hip-amdgcn-amd-amdhsa-<arch>.s with ROCm 7)
         asms = sorted(Path(tmp).glob(f"*amdgcn*{ARCH}*.s"))
-        if len(asms) != 1:
-            raise RuntimeError(f"expected one device assembly file from -save-temps, found {[a.name for a in asms]}")
-        return code_lengths(asms[0].read_text())
+        objs = sorted(Path(tmp).glob(f"*amdgcn*{ARCH}*.out"))
+        if len(asms) != 1 or len(objs) != 1:
+            raise RuntimeError(f"expected one device assembly and one linked device object from -save-temps, "
+                               f"found {[a.name for a in asms + objs]}")
+        estimates = code_lengths(asms[0].read_text())
+        funcs = elf_functions(objs[0].read_bytes())
+        lengths = {}
+        for name, estimate in estimates.items():
+            if name not in funcs:
+                raise RuntimeError(f"{name} is not in the linked device code object")
+            addr, size = funcs[name]
+            if addr % 256 or not 0 < size <= estimate:
+                raise RuntimeError(f"{name}: at {addr:#x}, {size} bytes (estimate {estimate})")
+            lengths[name] = size
+        return lengths
 
 
 def build(out: Path = OUT, defines: dict | None = None, verbose: bool = False) -> Path:

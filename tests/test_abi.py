@@ -215,3 +215,36 @@ def test_build_reads_code_lengths_and_checks_the_entry_pc():
         build.code_lengths(missing)
     with pytest.raises(RuntimeError, match="no code length"):
         build.code_lengths("".join(_asm(k, 0, 64) for k in names[:-1]))
+
+
+def test_build_reads_function_sizes_from_the_linked_object():
+    """The prefetch bound is the kernel's symbol size in the linked device
+    code object: a minimal ELF with a symbol table of two functions and one
+    object reads back as the two functions' (address, size)."""
+    import struct
+
+    import build
+
+    names = [b"", b"kern_a", b"kern_b", b"data_c"]
+    strtab = b"\0".join(names) + b"\0"
+    offs = [0]
+    for n in names[1:]:
+        offs.append(offs[-1] + len(names[len(offs) - 1]) + 1)
+    syms = struct.pack("<IBBHQQ", 0, 0, 0, 0, 0, 0)
+    syms += struct.pack("<IBBHQQ", offs[1], 0x12, 0, 1, 0x3100, 304572)   # FUNC
+    syms += struct.pack("<IBBHQQ", offs[2], 0x12, 0, 1, 0x95900, 280704)  # FUNC
+    syms += struct.pack("<IBBHQQ", offs[3], 0x11, 0, 1, 0x2000, 64)       # OBJECT
+    head = bytearray(64)
+    head[:6] = b"\x7fELF\x02\x01"
+    str_off = 64
+    sym_off = str_off + len(strtab)
+    sh_off = sym_off + len(syms)
+    struct.pack_into("<Q", head, 0x28, sh_off)
+    struct.pack_into("<HHH", head, 0x3A, 64, 3, 0)
+    sections = struct.pack("<IIQQQQIIQQ", 0, 0, 0, 0, 0, 0, 0, 0, 0, 0)
+    sections += struct.pack("<IIQQQQIIQQ", 0, 3, 0, 0, str_off, len(strtab), 0, 0, 1, 0)   # SHT_STRTAB
+    sections += struct.pack("<IIQQQQIIQQ", 0, 2, 0, 0, sym_off, len(syms), 1, 1, 8, 24)   # SHT_SYMTAB -> 1
+    data = bytes(head) + strtab + syms + sections
+    assert build.elf_functions(data) == {"kern_a": (0x3100, 304572), "kern_b": (0x95900, 280704)}
+    with pytest.raises(RuntimeError):
+        build.elf_functions(b"\x7fELF\x01\x01" + bytes(58))
