@@ -279,9 +279,6 @@ struct KParams {
     // bytes of the launched kernel's machine code that code_prefetch reads
     // into L2 (at most the kernel's length; 0: off)
     uint32_t code_len;
-    // opcode 2's claim form: one counter per layer, in the library scratch
-    // (null: the form is rejected)
-    int32_t *attn_claim;
     AttnParams attn_params;  // read only through attn_of()
 };
 
@@ -2317,33 +2314,13 @@ __device__ __forceinline__ bool partial_attn(kp_c &p, attn_c &a, SharedState &sh
 __device__ __forceinline__ bool op_partial_attn(kp_c &p, SharedState &sh, u32x4 *act, ins_t *ins, const Ctx &c,
                                 int32_t *tim) {
     const int layer = __builtin_amdgcn_readfirstlane(ins[1]);
-    int kv = __builtin_amdgcn_readfirstlane(ins[2]);
+    const int kv = __builtin_amdgcn_readfirstlane(ins[2]);
     const int nparts = __builtin_amdgcn_readfirstlane(ins[3]);
-    int pidx = __builtin_amdgcn_readfirstlane(ins[4]);
+    const int pidx = __builtin_amdgcn_readfirstlane(ins[4]);
     if (!need_attention(p, c, 2, layer)) return false;
     attn_c &a = attn_of(p);  // valid: attention tensors are present
-    const bool claim = kv == -1 && pidx == -1 && p.attn_claim != nullptr;
-    if (claim) {
-        // Claim form: take the layer's next partial, (kv, pidx) = divmod(j,
-        // nparts) for the j-th claim, or nothing once all Hkv * nparts are
-        // taken.  Workgroups claim as they finish their QKV blocks, so the
-        // partials go to the earliest ones and the last to finish QKV find
-        // none left, instead of holding up the stage with a partial that
-        // starts late.
-        if (layer < 0 || layer >= p.num_layers || nparts < 1 || nparts > a.P || a.skip_red) {
-            report_error(p, MK_ERR_BAD_INSTRUCTION, c, 2, layer, kv, pidx);
-            return false;
-        }
-        if (threadIdx.x == 0)
-            sh.flag = __hip_atomic_fetch_add(p.attn_claim + layer, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        const int j = __builtin_amdgcn_readfirstlane(sh.flag);
-        __syncthreads();
-        if (j >= a.Hkv * nparts) return true;
-        kv = j / nparts;
-        pidx = j - kv * nparts;
-    } else if (layer < 0 || layer >= p.num_layers || kv < 0 || kv >= a.Hkv || nparts < 1 || pidx < 0 ||
-               pidx >= nparts || (!a.skip_red && pidx >= a.P)) {
+    if (layer < 0 || layer >= p.num_layers || kv < 0 || kv >= a.Hkv || nparts < 1 || pidx < 0 || pidx >= nparts ||
+        (!a.skip_red && pidx >= a.P)) {
         report_error(p, MK_ERR_BAD_INSTRUCTION, c, 2, layer, kv, pidx);
         return false;
     }
@@ -3987,11 +3964,9 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
         lds_cap > stage_off ? std::min((size_t)MK_STAGE_ITEMS, (lds_cap - stage_off) / stage_item) : 0, g->late_loads);
     if (stage_items > 0) lds = std::max(lds, stage_off + stage_items * stage_item);
     // scratch: the work-claim slots, then the exit argmax's candidates (2
-    // ints per workgroup), opcode 2's claim counters (one per layer), then
-    // the spread counters
+    // ints per workgroup), then the spread counters
     const size_t cand = kScratchSlotBase + 2 * (size_t)g->num_workers * (size_t)g->queue_len;
-    const size_t claim = cand + 2 * (size_t)g->num_workers;  // opcode 2's claim counters, one per layer
-    const SpreadLayout sp = spread_layout(claim + (size_t)g->num_layers, g->num_layers, g->bar_ops,
+    const SpreadLayout sp = spread_layout(cand + 2 * (size_t)g->num_workers, g->num_layers, g->bar_ops,
                                           kSpreadDenseOps);
     rc = ensure_scratch(st, sp.end);
     if (rc != MK_OK) return rc;
@@ -4003,11 +3978,9 @@ int mk_llama_launch(const mk_llama_globals *g, void *stream) {
     kp.spread_rows = (int32_t)sp.rows;
     kp.spread_stride = (int32_t)sp.stride;
     kp.spread_ops = sp.ops;
-    // the last workgroup zeroes the claim slots, the candidates (after the
-    // exit argmax has read them) and the opcode-2 claim counters: every
-    // launch starts from zeroed scratch
-    kp.scratch_clear = (int32_t)(claim + (size_t)g->num_layers - kScratchSlotBase);
-    kp.attn_claim = st->scratch + claim;
+    // the last workgroup zeroes the claim slots and the candidates (after
+    // the exit argmax has read them): every launch starts from zeroed scratch
+    kp.scratch_clear = (int32_t)(cand + 2 * (size_t)g->num_workers - kScratchSlotBase);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
     kp.bar = g->barriers;
@@ -4153,15 +4126,13 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
                         : (attn ? reinterpret_cast<const void *>(mk_mixtral_kernel<0, true>)
                                 : reinterpret_cast<const void *>(mk_mixtral_kernel<0, false>));
     // scratch: exit counter, work-sharing cursors, then (overlap on) the
-    // column-chunk counters of every layer, then (attention launches)
-    // opcode 2's claim counters, one per layer
+    // column-chunk counters of every layer
     const size_t cursors = 2 * (size_t)g->num_workers * (size_t)g->queue_len;
     // compiled into the 8-expert MoE-only kernel only
     const bool overlap = g->downproj_overlap != 0 && !g->work_sharing && g->num_experts == 8 &&
                          g->qkv_weights == nullptr;
     const size_t chunks = overlap ? (size_t)g->num_layers * (size_t)(g->intermediate_size / 512) : 0;
-    const size_t claims = attn ? (size_t)g->num_layers : 0;
-    const SpreadLayout sp = spread_layout(kScratchSlotBase + cursors + chunks + claims, g->num_layers, g->bar_ops,
+    const SpreadLayout sp = spread_layout(kScratchSlotBase + cursors + chunks, g->num_layers, g->bar_ops,
                                           attn ? kSpreadMixtralOps : kSpreadMoeOps);
     int32_t *base = nullptr;
     if (noalloc) {
@@ -4179,8 +4150,7 @@ static int launch_mixtral(const mk_mixtral_globals *g, void *stream, bool noallo
     kp.spread_rows = (int32_t)sp.rows;
     kp.spread_stride = (int32_t)sp.stride;
     kp.spread_ops = sp.ops;
-    kp.scratch_clear = (int32_t)(cursors + chunks + claims);
-    kp.attn_claim = attn ? base + kScratchSlotBase + cursors + chunks : nullptr;
+    kp.scratch_clear = (int32_t)(cursors + chunks);
     kp.instructions = g->instructions;
     kp.timings = g->record_timings ? g->timings : nullptr;
     kp.bar = g->barriers;

@@ -20,8 +20,7 @@ Counterpart of ``megakernels/demos/latency/scheduler.py:1-440``:
   faster than the 8-row ones that balance the row count (at 3B and 256
   workers: 24 rows on every worker instead of 32 on some and 16 on others).
   The split-KV partition count follows the MI355X policy of the Mixtral
-  scheduler, and so do the claimed partials (``partial_claims``);
-  ``attention_partitions="reference"`` restores the reference's.
+  scheduler; ``attention_partitions="reference"`` restores the reference's.
 
 The reference asserts more than one block per worker in every partitioner
 (it targets 132-160 SMs and 1B/3B shapes); here a partitioner with fewer
@@ -38,8 +37,7 @@ import torch
 from ..instructions import NoOp
 from ..scheduler import DAG_Node, ScheduleBuilder
 from ..utils import assert_div, get_sm_count
-from ..mixtral.scheduler import (partial_attention_nodes, pick_block_size, pick_num_attention_partitions,
-                                 reduction_deps)
+from ..mixtral.scheduler import pick_block_size, pick_num_attention_partitions
 from .instructions import (
     AttentionReduction,
     DownProjResidual,
@@ -80,16 +78,13 @@ def default_down_block_size(hidden: int, workers: int, reduction: int, intermedi
 
 def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 0,
                  sm_count: int | None = None, attention_partitions: str = "mi355x",
-                 qkv_block_size: int | None = None, partial_claims: bool = True, **block_sizes) -> Globals:
+                 qkv_block_size: int | None = None, **block_sizes) -> Globals:
     """Activation buffers plus ``model``'s stacked weights (duck-typed like
     the reference's ``LlamaForCausalLM``); ``sm_count`` overrides the device
     query (needed when the globals live on the CPU); ``attention_partitions``
     is the split-KV partition policy (the Mixtral scheduler's
     ``pick_num_attention_partitions``; ``"reference"`` reproduces the
-    reference's instruction list); ``partial_claims`` has the partials
-    claimed by the workers as they finish QKV (MI355X policy only; the
-    Mixtral scheduler's ``partial_attention_nodes``).  ``block_sizes``
-    override the defaults of
+    reference's instruction list).  ``block_sizes`` override the defaults of
     ``up_gate_proj_block_size``, ``down_proj_block_size``,
     ``o_proj_block_size``, ``lm_head_block_size`` and
     ``matvec_reduction_size``."""
@@ -162,7 +157,6 @@ def make_globals(model, skip_attn_reduction: bool | None = None, seq_len: int = 
     )
     globs.sm_count_override = sm_count
     globs.attn_partition_policy = attention_partitions
-    globs.attn_partial_claims = bool(partial_claims)
     return globs
 
 
@@ -248,8 +242,14 @@ def make_dag_layer(globs: Globals, layer_idx: int, prev_layer_outputs, stop_afte
     if stop_after_op == "qkv":
         return nodes, qkv_nodes
 
-    assert_div(globs.head_dim, globs.qkv_block_size)
-    partial_nodes = partial_attention_nodes(globs, layer_idx, parts, by_block, PartialAttention)
+    bph = assert_div(globs.head_dim, globs.qkv_block_size)
+    partial_nodes = []
+    for kv in range(globs.num_kv_heads):
+        k0 = (globs.num_attention_heads + kv) * globs.head_dim // globs.qkv_block_size
+        v0 = (globs.num_attention_heads + globs.num_kv_heads + kv) * globs.head_dim // globs.qkv_block_size
+        deps = {id(by_block[b]): by_block[b] for b in [*range(k0, k0 + bph), *range(v0, v0 + bph)]}
+        for p in range(parts):
+            partial_nodes.append(DAG_Node(PartialAttention(layer_idx, kv, parts, p), list(deps.values())))
     nodes.extend(partial_nodes)
     if stop_after_op == "partial":
         return nodes, partial_nodes
@@ -259,7 +259,7 @@ def make_dag_layer(globs: Globals, layer_idx: int, prev_layer_outputs, stop_afte
         red_nodes = []
         for kv in range(globs.num_kv_heads):
             ins = AttentionReduction(layer_idx, kv * gqa, parts, True, list(range(parts)), None)
-            red_nodes.append(DAG_Node(ins, reduction_deps(partial_nodes, kv)))
+            red_nodes.append(DAG_Node(ins, [n for n in partial_nodes if n.instruction.kv_head_idx == kv]))
         nodes.extend(red_nodes)
         oproj_deps = red_nodes
     else:

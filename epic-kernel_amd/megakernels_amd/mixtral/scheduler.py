@@ -37,20 +37,6 @@ Differences, all MI355X-motivated and recorded here:
   output as they complete instead of after the layer's last opcode-5 block).
   Indices, scores and barrier counts are unchanged; hidden states differ
   only in the fp32 summation order of the down-projection rows.
-* under the MI355X partition policy the partials can be claimed instead of
-  assigned (``partial_claims=True``; the dense scheduler's default, off here):
-  a layer's opcode-2 instructions become ``W - kv_heads - 1`` claim
-  instructions (``kv_head_idx`` and ``partial_idx`` -1,
-  :func:`partial_attention_nodes`), one per worker that runs neither a
-  reduction nor the layer's opcode 8, and the j-th to run takes partial
-  ``divmod(j, num_partials)`` from a per-layer counter in the library
-  scratch, or nothing once all are taken.  Workers claim as they finish
-  their QKV blocks, so those that finish QKV last (whose partials end the
-  stage) are the ones left without a partial.  Every partial is still
-  computed exactly once, so results and barrier counts are unchanged.
-  Same-process A/B: config 3 +0.5 %, config 4 level, config 5 -1.0 %
-  (there every claimer gets a partial, and the claim's round trip delays
-  the K/V staging).
 * ``make_moe_dag`` builds the MoE-only slice of one layer (optional opcode 8,
   then opcode 5 and opcode 6) for running the hot path in isolation; the
   attention prefix it skips is represented by pre-filling the O-proj barrier
@@ -133,39 +119,6 @@ def pick_num_attention_partitions(prompt_len: int, ntok: int, num_kv_heads: int,
     return max(1, math.ceil(total / math.ceil(total / n)))
 
 
-def partial_attention_nodes(globs, layer_idx: int, parts: int, by_block, make_ins, reserved: int = 0):
-    """Opcode-2 DAG nodes of one layer: one instruction per (KV head,
-    partition), each after its head's K and V blocks -- or, with
-    ``globs.attn_partial_claims`` under the MI355X policy and more than one
-    partition, ``max(W - kv_heads - reserved, kv_heads * parts)`` claim
-    instructions (KV head and partition -1) after all of the layer's QKV
-    blocks.  ``reserved`` counts the layer's instructions placed between the
-    QKV blocks and the partials (opcode 8): with round-robin assignment the
-    claims, the reductions and those then take one worker each.
-    ``make_ins(layer, kv, parts, p)`` builds one instruction."""
-    hkv = globs.num_kv_heads
-    claims = (getattr(globs, "attn_partial_claims", False) and parts > 1
-              and getattr(globs, "attn_partition_policy", "reference") != "reference")
-    if claims:
-        deps = list({id(n): n for n in by_block.values()}.values())
-        n = max(globs.sm_count() - hkv - reserved, hkv * parts)
-        return [DAG_Node(make_ins(layer_idx, -1, parts, -1), deps) for _ in range(n)]
-    bph = globs.head_dim // globs.qkv_block_size
-    nodes = []
-    for kv in range(hkv):
-        k0 = (globs.num_attention_heads + kv) * globs.head_dim // globs.qkv_block_size
-        v0 = (globs.num_attention_heads + hkv + kv) * globs.head_dim // globs.qkv_block_size
-        deps = {id(by_block[b]): by_block[b] for b in [*range(k0, k0 + bph), *range(v0, v0 + bph)]}
-        for p in range(parts):
-            nodes.append(DAG_Node(make_ins(layer_idx, kv, parts, p), list(deps.values())))
-    return nodes
-
-
-def reduction_deps(partial_nodes, kv: int):
-    """The partial nodes a KV head's reduction waits for (every claim node)."""
-    return [n for n in partial_nodes if n.instruction.kv_head_idx in (kv, -1)]
-
-
 def pick_block_size(rows: int, workers: int, candidates=(16, 8, 4)) -> int:
     """Row-block size that minimises the busiest worker's row count when
     ``rows / block`` blocks are spread over ``workers`` (ties -> larger
@@ -195,7 +148,6 @@ def make_globals(
     qkv_block_size: int | None = None,
     moe_overlap: bool = False,
     upgate_rounds: int = 3,
-    partial_claims: bool = False,
 ) -> MixtralGlobals:
     """Allocate activation buffers and wrap ``model``'s stacked weights.
 
@@ -211,9 +163,6 @@ def make_globals(
     reference's instruction list).  ``moe_overlap`` selects the interleaved
     opcode-5 partition (:func:`schedule_rms_router_upgate`) and has
     ``interpret_with_mk`` launch with the opcode-5/6 overlap.
-    ``partial_claims`` (MI355X partition policy only) has the partials
-    claimed by the workers as they finish QKV
-    (:func:`partial_attention_nodes`).
     """
     cfg = model.config
     device = torch.device(model.device)
@@ -299,7 +248,6 @@ def make_globals(
     )
     globs.sm_count_override = sm_count
     globs.attn_partition_policy = attention_partitions
-    globs.attn_partial_claims = bool(partial_claims)
     globs.moe_overlap = bool(moe_overlap)
     globs.upgate_rounds = int(upgate_rounds)
     return globs
@@ -413,8 +361,14 @@ def make_dag_layer(globs: MixtralGlobals, layer_idx: int, prev_layer_outputs, st
     if stop_after_op == "qkv":
         return nodes, qkv_nodes
 
-    partial_nodes = partial_attention_nodes(globs, layer_idx, parts, by_block, Mixtral_PartialAttn,
-                                            reserved=1 if predict else 0)
+    bph = globs.head_dim // globs.qkv_block_size
+    partial_nodes = []
+    for kv in range(globs.num_kv_heads):
+        k0 = (globs.num_attention_heads + kv) * globs.head_dim // globs.qkv_block_size
+        v0 = (globs.num_attention_heads + globs.num_kv_heads + kv) * globs.head_dim // globs.qkv_block_size
+        deps = {id(by_block[b]): by_block[b] for b in [*range(k0, k0 + bph), *range(v0, v0 + bph)]}
+        for p in range(parts):
+            partial_nodes.append(DAG_Node(Mixtral_PartialAttn(layer_idx, kv, parts, p), list(deps.values())))
     nodes.extend(partial_nodes)
     if stop_after_op == "partial":
         return nodes, partial_nodes
@@ -424,7 +378,7 @@ def make_dag_layer(globs: MixtralGlobals, layer_idx: int, prev_layer_outputs, st
         red_nodes = []
         for kv in range(globs.num_kv_heads):
             ins = Mixtral_AttnReduction(layer_idx, kv * gqa, parts, True, list(range(parts)), None)
-            red_nodes.append(DAG_Node(ins, reduction_deps(partial_nodes, kv)))
+            red_nodes.append(DAG_Node(ins, [n for n in partial_nodes if n.instruction.kv_head_idx == kv]))
         nodes.extend(red_nodes)
         oproj_deps = red_nodes
     else:

@@ -47,7 +47,6 @@ _PKG = _REPO / "epic-kernel_amd"
 if str(_PKG) not in sys.path:
     sys.path.insert(0, str(_PKG))
 
-import dataclasses  # noqa: E402
 import math  # noqa: E402
 
 from megakernels_amd.mixtral.instructions import (  # noqa: E402
@@ -392,29 +391,8 @@ def partial_token_range(seq_len: int, kv_block_size: int, num_partials: int, par
     return b0 * kv_block_size, min(b1 * kv_block_size, seq_len)
 
 
-def claim_partial(globs, ins):
-    """(kv_head, partial) of a claim-form opcode 2 (KV head and partition
-    -1, an MI355X schedule extension with no reference counterpart): the
-    j-th claim of a layer takes partial ``divmod(j, num_partials)``, or
-    nothing (None) once all ``kv_heads * num_partials`` are taken.  Claims
-    are counted per ``interpret_with_pyvm`` call, in list order; the kernel
-    counts them in the order workgroups reach them, and since each partial
-    is computed once either way, the results do not depend on the order."""
-    claims = globs.__dict__.setdefault("_attn_claims", {})
-    j = claims.get(ins.layer_idx, 0)
-    claims[ins.layer_idx] = j + 1
-    if j >= globs.num_kv_heads * ins.num_partials:
-        return None
-    return divmod(j, ins.num_partials)
-
-
 def solve_partial_attn(globs: MixtralGlobals, ins: Mixtral_PartialAttn):
-    """mkm/python_vm.py:125-159 (claim form: :func:`claim_partial`)."""
-    if ins.kv_head_idx == -1 and ins.partial_idx == -1:
-        job = claim_partial(globs, ins)
-        if job is None:
-            return
-        ins = dataclasses.replace(ins, kv_head_idx=job[0], partial_idx=job[1])
+    """mkm/python_vm.py:125-159."""
     gqa = globs.num_attention_heads // globs.num_kv_heads
     bph = globs.head_dim // globs.qkv_block_size
     layer, kv = ins.layer_idx, ins.kv_head_idx
@@ -512,7 +490,6 @@ def interpret_with_pyvm(globs, instructions, instruction_to_solver=None):
     """Run the linear (topological) instruction list sequentially
     (megakernels/python_vm.py:83-87)."""
     table = INSTRUCTION_TO_SOLVER if instruction_to_solver is None else instruction_to_solver
-    globs.__dict__["_attn_claims"] = {}  # claim-form opcode 2 counts per call
     for ins in instructions:
         table[type(ins)](globs, ins)
 

@@ -131,12 +131,10 @@ def _check_stage(tag, case, exact_keys, one_ulp=()):
 # configs 4 and 5: two-layer slices of the Mixtral-8x7B shape
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("prefill,sigma,claims", [(4096, None, False), (16384, 0.007, False), (4096, None, True)],
-                         ids=["c4", "c5", "c4-claims"])
-def test_mixtral_two_layers_at_config_shape(prefill, sigma, claims):
+@pytest.mark.parametrize("prefill,sigma", [(4096, None), (16384, 0.007)], ids=["c4", "c5"])
+def test_mixtral_two_layers_at_config_shape(prefill, sigma):
     case = FullCase(with_layers(C4, 2), seed=40, prefill=prefill, steps=3, generate_on_device=True,
-                    ln_weight_std=0.1, predictor_sigma=sigma, partial_claims=claims)
-    assert any(i.opcode() == 2 and i.kv_head_idx == -1 for i in case.linear) == claims
+                    ln_weight_std=0.1, predictor_sigma=sigma)
     parts = max(i.num_partials for i in case.linear if i.opcode() == 2)
     print(f"[c4-shape x2, {prefill} cached] {len(case.linear)} instructions, {parts} partitions per KV head",
           flush=True)
@@ -150,11 +148,8 @@ def test_mixtral_two_layers_at_config_shape(prefill, sigma, claims):
 # config 3: two-layer slice of the Llama-3.2-3B shape (dense VM)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("claims", [True, False], ids=["claims", "static"])
-def test_llama_two_layers_at_config_shape(claims):
-    case = LlamaCase(with_layers(C3, 2), seed=41, prefill=2048, steps=3, generate_on_device=True,
-                     partial_claims=claims)
-    assert any(i.opcode() == 2 and i.kv_head_idx == -1 for i in case.linear) == claims
+def test_llama_two_layers_at_config_shape():
+    case = LlamaCase(with_layers(C3, 2), seed=41, prefill=2048, steps=3, generate_on_device=True)
     for tok in (5, 64000, 128255):
         case.step(tok)
         _check_through("c3 x2", case)

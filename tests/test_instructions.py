@@ -230,66 +230,3 @@ def test_moe_dag():
         assert len(queues) == 16
         assert sorted(i.serialize() for q in queues for i in q) == sorted(
             i.serialize() for i in sched.get_linear_instructions())
-
-
-def _claim_globals(claims: bool, workers: int = 16, prefill: int = 600):
-    model = make_synthetic_mixtral(with_layers(SMALL, 2), "cpu", 3, full=True, kv_positions=prefill + 2,
-                                   prefill=prefill)
-    g = make_globals(model, sm_count=workers, seq_len=prefill, partial_claims=claims)
-    assert not make_globals(model, sm_count=workers, seq_len=prefill).attn_partial_claims  # off by default here
-    g.pos_id = prefill
-    return model, g
-
-
-def test_claimed_partials_structure():
-    """Under the MI355X policy each layer's partials become W - kv_heads - 1
-    claim instructions ([2, layer, -1, parts, -1]; one worker is left for the
-    layer's opcode 8); the reference policy and partial_claims=False keep one
-    instruction per (KV head, partition)."""
-    _, g = _claim_globals(True)
-    parts = pick_num_attention_partitions(601, 0, 2, 16, "mi355x")
-    assert parts > 1 and 2 * parts <= 16 - 2
-    nodes, _ = make_dag(g)
-    for layer in range(2):
-        ops2 = [n for n in nodes if n.instruction.opcode() == 2 and n.instruction.layer_idx == layer]
-        assert len(ops2) == 16 - 2 - 1
-        assert all(n.instruction.serialize() == [2, layer, -1, parts, -1] for n in ops2)
-        qkv = {id(n) for n in nodes if n.instruction.opcode() == 1 and n.instruction.layer_idx == layer}
-        assert all({id(d) for d in n.dependencies} == qkv for n in ops2)
-        reds = [n for n in nodes if n.instruction.opcode() == 3 and n.instruction.layer_idx == layer]
-        assert len(reds) == 2 and all(len(r.dependencies) == 16 - 3 for r in reds)
-    # round robin: one claim, reduction or opcode 8 per worker and layer
-    queues = assign_to_sms("rr", schedule=Schedule(g, *make_dag(g)))
-    for layer in range(2):
-        per_worker = [sum(1 for i in q if i.opcode() in (2, 3, 8) and i.layer_idx == layer) for q in queues]
-        assert per_worker == [1] * 16
-    assert len([n for n in make_dag(g, predict=False)[0] if n.instruction.opcode() == 2]) == 2 * (16 - 2)
-    _, g = _claim_globals(False)
-    ops = [n.instruction for n in make_dag(g)[0] if n.instruction.opcode() == 2]
-    assert sorted((i.layer_idx, i.kv_head_idx, i.partial_idx) for i in ops) == [
-        (layer, kv, p) for layer in range(2) for kv in range(2) for p in range(parts)]
-    model = make_synthetic_mixtral(with_layers(SMALL, 2), "cpu", 3, full=True, kv_positions=602, prefill=600)
-    g = make_globals(model, sm_count=16, seq_len=600, attention_partitions="reference")
-    assert all(n.instruction.kv_head_idx >= 0 for n in make_dag(g)[0] if n.instruction.opcode() == 2)
-
-
-def test_claimed_partials_oracle_matches_static():
-    """The oracle runs the claim form's j-th claim as partial divmod(j,
-    parts) and skips the claims past the last partial: a whole two-layer
-    step over the claim schedule leaves every tensor bit-identical to the
-    static schedule's, barriers included."""
-    from oracle import python_vm as oracle
-
-    states = []
-    for claims in (False, True):
-        model, g = _claim_globals(claims)
-        g.hidden_states.copy_(model.embed_tokens[5])
-        linear = Schedule(g, *make_dag(g)).get_linear_instructions()
-        assert any(i.opcode() == 2 and i.kv_head_idx == -1 for i in linear) == claims
-        oracle.interpret_with_pyvm(g, linear)
-        states.append(g)
-    a, b = states
-    for name in ("hidden_states", "post_ln_rope_q", "attn_out", "attn_out_intermediates", "attn_lse_intermediates",
-                 "logits", "barriers", "k_cache", "v_cache", "selected_expert_indices"):
-        assert torch.equal(getattr(a, name), getattr(b, name)), name
-    assert b.attn_out.float().abs().sum() > 0 and b.attn_lse_intermediates.abs().sum() > 0
