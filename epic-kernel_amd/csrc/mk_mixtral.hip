@@ -2482,20 +2482,26 @@ __device__ __forceinline__ bool op_attn_reduction(kp_c &p, SharedState &sh, u32x
 // waits for the attention reduction, else by opcode 5 itself before its own
 // wait.  Opcode 5 then starts on them the moment its wait ends.  Layout:
 // item i, matrix j (0 gate, 1 up), chunk c is the 1 KiB at u32x4 index
-// stage_off16 + ((2 i + j) nc + c) 64, lane order.  The loads complete
-// before the workgroup passes its next barrier.
-__device__ __forceinline__ void stage_dense_upgate(kp_c &p, SharedState &sh, u32x4 *act,
-                                                   ins_t *nx, int slot, int layer) {
-    if (p.stage_items <= 0 || slot >= p.queue_len) return;
+// stage_off16 + ((2 i + j) nc + c) 64, lane order; item i is staged by wave
+// i mod kWaves, which is also the wave that computes it.  The loads
+// complete before the workgroup passes its next barrier.  Returns the items
+// staged (uniform).  `publish` (opcode 4, for the next instruction) records
+// them in sh.stage_slot / sh.stage_n for opcode 5 to find; opcode 5 staging
+// its own items uses the return value, since its waves read sh.stage_slot
+// at their own pace and a wave that saw it change would skip the staging
+// and fall one workgroup barrier out of step with the others.
+__device__ __forceinline__ int stage_dense_upgate(kp_c &p, SharedState &sh, u32x4 *act, ins_t *nx, int slot,
+                                                  int layer, bool publish) {
+    if (p.stage_items <= 0 || slot >= p.queue_len) return 0;
     const int op = __builtin_amdgcn_readfirstlane(nx[0]);
     const int l = __builtin_amdgcn_readfirstlane(nx[1]);
     const int n = __builtin_amdgcn_readfirstlane(nx[2]);
-    if (op != 5 || l != layer || n < 1 || n > MK_INTS_PER_INSTRUCTION - 3) return;
+    if (op != 5 || l != layer || n < 1 || n > MK_INTS_PER_INSTRUCTION - 3) return 0;
     const int S = min(p.stage_items, n * p.expert_bs);
     const int nblocks = p.F / p.expert_bs;
     for (int k = 0; k * p.expert_bs < S; ++k) {
         const int b = __builtin_amdgcn_readfirstlane(nx[3 + k]);
-        if (b < 0 || b >= nblocks) return;  // opcode 5 reports it
+        if (b < 0 || b >= nblocks) return 0;  // opcode 5 reports it
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nc = p.H / kChunkElems;
@@ -2513,10 +2519,11 @@ __device__ __forceinline__ void stage_dense_upgate(kp_c &p, SharedState &sh, u32
                                              0, 0);
         }
     }
-    if (threadIdx.x == 0) {
+    if (publish && threadIdx.x == 0) {
         sh.stage_slot = slot;
         sh.stage_n = S;
     }
+    return S;
 }
 
 // Mixtral whole-model launches: the first items (a gate row and an up row
@@ -2605,7 +2612,7 @@ __device__ __forceinline__ bool op_oproj(kp_c &p, SharedState &sh, u32x4 *act, i
     if (!ostaged) {
         pair_ahead_load(pre, wo, (size_t)K, 0, K / kChunkElems, r0, nrows);
         if (p.E == 1)
-            stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
+            (void)stage_dense_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer, true);
         else
             stage_moe_upgate(p, sh, act, ins + MK_INTS_PER_INSTRUCTION, c.slot + 1, layer);
     }
@@ -2797,13 +2804,11 @@ __device__ __forceinline__ bool op_dense_upgate(kp_c &p, SharedState &sh, u32x4 
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int items = n * p.expert_bs, nc = p.H / kChunkElems;
-    // items [0, S) staged in LDS: by the preceding opcode 4, else here
+    // items [0, S) staged in LDS: by the preceding opcode 4 (which left
+    // sh.stage_slot / sh.stage_n set before its barriers), else here
     const bool pre_staged = __builtin_amdgcn_readfirstlane(sh.stage_slot) == c.slot;
-    if (!pre_staged) {
-        stage_dense_upgate(p, sh, act, ins, c.slot, layer);
-        __syncthreads();
-    }
-    const int S = __builtin_amdgcn_readfirstlane(sh.stage_slot == c.slot ? sh.stage_n : 0);
+    const int S = pre_staged ? __builtin_amdgcn_readfirstlane(sh.stage_n)
+                             : stage_dense_upgate(p, sh, act, ins, c.slot, layer, false);
     if (threadIdx.x == 0) sh.next_item = S + kWaves;
     // each wave's first item from HBM (its gate and up rows) is loaded
     // before the wait: the weights do not depend on it (issued after the
