@@ -57,11 +57,11 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes moved per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE per
 # dispatch, each scaled by what the same counter reads for a device copy of
 # known size: FETCH x 2.0, WRITE x 1.0), measured on the kernel of commit
-# 86ab2dc: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
+# 0e3b696: config 2 one MoE layer; configs 3/4/5 one decode step at 2050 /
 # 4098 / 16386 cached positions.  The counter runs are summarised under
 # profiles/.
-MEASURED_TRAFFIC_BYTES = {"c2": 707_881_665, "c3": 6_749_121_167, "c4": 26_288_531_362, "c5": 28_034_579_492}
-TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 86ab2dc; "
+MEASURED_TRAFFIC_BYTES = {"c2": 707_841_102, "c3": 6_749_136_490, "c4": 26_290_541_573, "c5": 28_033_287_742}
+TRAFFIC_UNIT = ("bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, kernel of commit 0e3b696; "
                 "configs 3-5 at 2050 / 4098 / 16386 cached positions)")
 
 
